@@ -1,0 +1,134 @@
+/*
+ * msda.h — C ABI of the MI355X (gfx950) multi-scale deformable attention library.
+ *
+ * One shared library, libmsda_hip.so, exports these entry points. They take plain
+ * device pointers, sizes and a hipStream_t passed as void*; no torch or HIP types
+ * appear in the signatures, so any FFI (ctypes, cffi, pybind11, a C++ caller) can bind
+ * them. The Python package msda_triton binds them through ctypes.
+ *
+ * Tensor contract (identical to msda_triton's, reference README.md:60-68):
+ *   value               (B, K, H, C)        value_dtype, contiguous
+ *   spatial_shapes      (L, dim)  int32     device memory; rows are (H_l, W_l) for dim 2
+ *                                           and (D_l, H_l, W_l) for dim 3
+ *   level_start         (L,)      int32     device memory; exclusive prefix sum of the
+ *                                           per-level sizes (row-major flattening of K)
+ *   sampling_locations  (B, Q, H, L, P, dim) coord_dtype, contiguous, order (x, y[, z])
+ *                                           with x along W, y along H, z along D
+ *   attention_weights   (B, Q, H, L, P)      coord_dtype, contiguous
+ *   output              (B, Q, H*C)          value_dtype, contiguous
+ *
+ * Every call returns an msda_status. On failure, msda_last_error() returns a
+ * thread-local message that names the failing check. Calls enqueue work on `stream`
+ * and do not synchronise. Calls on different streams or threads are independent:
+ * the library holds no mutable global state apart from the thread-local error text.
+ */
+#ifndef MSDA_H_
+#define MSDA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MSDA_ABI_VERSION 1
+
+typedef enum msda_dtype {
+  MSDA_F32 = 0,
+  MSDA_F16 = 1,
+  MSDA_BF16 = 2
+} msda_dtype;
+
+typedef enum msda_status {
+  MSDA_OK = 0,
+  MSDA_ERR_INVALID = 1,         /* a size, pointer or flag is out of range */
+  MSDA_ERR_DTYPE = 2,           /* unsupported dtype or dtype combination */
+  MSDA_ERR_WORKSPACE = 3,       /* workspace missing or too small */
+  MSDA_ERR_HIP = 4              /* a HIP runtime call failed (launch error) */
+} msda_status;
+
+/* Problem descriptor shared by forward and backward. All counts are element counts. */
+typedef struct msda_desc {
+  int32_t dim;          /* 2: bilinear over (H, W); 3: trilinear over (D, H, W) */
+  int32_t batch;        /* B */
+  int64_t num_keys;     /* K = sum over levels of prod(shape_l) */
+  int32_t num_heads;    /* H */
+  int32_t channels;     /* C, channels per head */
+  int64_t num_queries;  /* Q */
+  int32_t num_levels;   /* L */
+  int32_t num_points;   /* P */
+  int32_t value_dtype;  /* msda_dtype of value, output, grad_output and grad_value */
+  int32_t coord_dtype;  /* msda_dtype of sampling_locations, attention_weights and their
+                           gradients; must equal value_dtype or be MSDA_F32 */
+  int32_t clamp_grid;   /* nonzero: clamp the [-1, 1] sampling grid to [-1+eps, 1-eps] */
+  int32_t reserved;     /* must be 0 */
+  double clamp_eps;     /* eps of the clamp above (reference default 1e-4) */
+} msda_desc;
+
+/* ABI version of the loaded library (MSDA_ABI_VERSION it was built with). */
+int msda_abi_version(void);
+
+/* Thread-local text of the last error raised on this thread ("" if none). */
+const char* msda_last_error(void);
+
+/*
+ * Host-only validation of a descriptor: sizes, dtypes and 32-bit index limits.
+ * Touches no device. msda_fwd and msda_bwd run the same checks first.
+ */
+int msda_validate(const msda_desc* desc);
+
+/*
+ * Forward: output = sum_l sum_p attn[b,q,h,l,p] * sample(value[b, level l, h, :], loc[b,q,h,l,p])
+ * with bilinear (dim 2) or trilinear (dim 3) sampling, zero padding outside the level,
+ * align_corners=False, fp32 accumulation, and output rounded once to value_dtype.
+ *
+ * Replaces the reference's _fwd_kernel_2d launch and permute/cast epilogue
+ * (src/msda_triton/triton/msda_2d.py:606-651) and the 3D equivalent
+ * (src/msda_triton/triton/msda_3d.py:749-794).
+ */
+int msda_fwd(const msda_desc* desc,
+             const void* value,
+             const int32_t* spatial_shapes,
+             const int32_t* level_start,
+             const void* sampling_locations,
+             const void* attention_weights,
+             void* output,
+             void* stream);
+
+/*
+ * Bytes of device workspace msda_bwd needs for this descriptor: 0 for fp32 value,
+ * B*K*H*C*4 (an fp32 grad_value accumulator) for fp16/bf16 value.
+ */
+size_t msda_bwd_workspace_bytes(const msda_desc* desc);
+
+/*
+ * Backward of msda_fwd with respect to value, sampling_locations and attention_weights.
+ * grad_value is fully overwritten (the library clears it, or its fp32 workspace, on
+ * `stream` with a fill kernel), as are grad_sampling_locations and
+ * grad_attention_weights. Gradients of clamped grid coordinates are zero, matching the
+ * backward of torch.clamp. grad_value accumulates with device atomics, so its low-order
+ * bits depend on execution order.
+ *
+ * Replaces the reference's MSDA2DFn.backward body (src/msda_triton/triton/msda_2d.py:778-853)
+ * and MSDA3DFn.backward (src/msda_triton/triton/msda_3d.py:920-996).
+ */
+int msda_bwd(const msda_desc* desc,
+             const void* value,
+             const int32_t* spatial_shapes,
+             const int32_t* level_start,
+             const void* sampling_locations,
+             const void* attention_weights,
+             const void* grad_output,
+             void* grad_value,
+             void* grad_sampling_locations,
+             void* grad_attention_weights,
+             void* workspace,
+             size_t workspace_bytes,
+             void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MSDA_H_ */

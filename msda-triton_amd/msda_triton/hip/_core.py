@@ -1,0 +1,235 @@
+"""Host layer shared by the 2D and 3D HIP ops: validation, level tables, C-ABI calls.
+
+Mirrors the reference's host side for this path (src/msda_triton/triton/msda_2d.py:17-82,
+541-651, 721-853 and src/msda_triton/triton/msda_3d.py:17-77, 684-794, 864-996): the same
+checks with the same exception types and messages, the same CPU- versus GPU-resident
+spatial-shape handling, and the same autograd contract. The kernels themselves live in
+libmsda_hip.so (csrc/msda_kernels.hip) and are reached through include/msda.h.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from collections import OrderedDict
+
+import torch
+
+from .. import _lib
+
+_DTYPE_CODE = {torch.float32: _lib.MSDA_F32, torch.float16: _lib.MSDA_F16,
+               torch.bfloat16: _lib.MSDA_BF16}
+_COORD_NAMES = {2: "(B, Q, H, L, P, 2)", 3: "(B, Q, H, L, P, 3)"}
+_SHAPE_NAMES = {2: "H_l x W_l", 3: "D_l x H_l x W_l"}
+_INT32_MAX = 2**31 - 1
+
+# Device copies of CPU-resident level tables, keyed by (dim, shapes, device).
+_LEVEL_CACHE: OrderedDict = OrderedDict()
+_LEVEL_CACHE_MAX = 64
+
+
+def validate_inputs(name: str, dim: int, value: torch.Tensor, value_spatial_shapes: torch.Tensor,
+                    sampling_locations: torch.Tensor, attention_weights: torch.Tensor) -> None:
+    """Device, dtype and shape checks; raises on the first violation.
+
+    Same order, types and messages as _validate_inputs_2d (triton/msda_2d.py:541-583) and
+    _validate_inputs_3d (triton/msda_3d.py:684-726), plus a same-device check.
+    """
+    if not value.is_cuda:
+        raise ValueError(f"{name} HIP kernel requires CUDA tensors. Got CPU tensors instead.")
+    if value.dtype not in _DTYPE_CODE:
+        raise NotImplementedError(
+            f"{name} HIP kernel only supports fp32, fp16, and bf16. Got {value.dtype}. "
+            "The kernel accumulates in fp32 internally."
+        )
+    if value.dim() != 4:
+        raise ValueError(f"value must be (B, K, H, C), got {tuple(value.shape)}")
+    if sampling_locations.dim() != 6:
+        raise ValueError(
+            f"sampling_locations must be {_COORD_NAMES[dim]}, got {tuple(sampling_locations.shape)}"
+        )
+    bsz, _, num_heads, _ = value.shape
+    bsz_s, num_queries, num_heads_s, num_levels, num_points, last = sampling_locations.shape
+    if not (bsz == bsz_s and num_heads == num_heads_s and last == dim):
+        raise ValueError(
+            f"Shape mismatch: value=(B,K,H,C), sampling_locations={_COORD_NAMES[dim].replace(' ', '')}. "
+            f"Got value={tuple(value.shape)}, sampling_locations={tuple(sampling_locations.shape)}"
+        )
+    if attention_weights.shape != (bsz, num_queries, num_heads, num_levels, num_points):
+        raise ValueError(
+            f"attention_weights must be (B,Q,H,L,P), got {tuple(attention_weights.shape)}"
+        )
+    if value_spatial_shapes.shape != (num_levels, dim):
+        raise ValueError(
+            f"value_spatial_shapes must be (L,{dim}), got {tuple(value_spatial_shapes.shape)}. "
+            f"num_levels={num_levels}, expected shape=({num_levels}, {dim})"
+        )
+    for tname, t in (("sampling_locations", sampling_locations),
+                     ("attention_weights", attention_weights)):
+        if t.device != value.device:
+            raise ValueError(f"{tname} is on {t.device} but value is on {value.device}")
+        if not t.is_floating_point():
+            raise ValueError(f"{tname} must be a floating-point tensor, got {t.dtype}")
+
+
+def prepare_levels(dim: int, value: torch.Tensor,
+                   value_spatial_shapes: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(L, dim) int32 shapes and (L,) int32 level starts on value's device.
+
+    CPU-resident shapes are checked against K and the int32 range (as in
+    _prepare_spatial_2d, triton/msda_2d.py:53-74) and their device copy is cached.
+    GPU-resident shapes are converted on the device without a host sync and without the
+    K check (triton/msda_2d.py:76-82).
+    """
+    device = value.device
+    if value_spatial_shapes.device.type == "cpu":
+        shapes_cpu = value_spatial_shapes.detach().to(dtype=torch.int64)
+        rows = tuple(tuple(int(v) for v in r) for r in shapes_cpu.tolist())
+        key = (dim, rows, device)
+        hit = _LEVEL_CACHE.get(key)
+        sizes = [1] * len(rows)
+        for i, r in enumerate(rows):
+            for v in r:
+                sizes[i] *= v
+        total_keys = sum(sizes)
+        if total_keys > _INT32_MAX:
+            raise ValueError(
+                f"Total number of keys ({total_keys}) exceeds int32 range. "
+                "Reduce spatial dimensions or number of levels."
+            )
+        if value.size(1) != total_keys:
+            raise ValueError(
+                f"value dim 1 ({value.size(1)}) does not match sum of spatial shapes "
+                f"({total_keys}). Ensure K = Σ({_SHAPE_NAMES[dim]}) across all levels."
+            )
+        if hit is not None:
+            _LEVEL_CACHE.move_to_end(key)
+            return hit
+        starts = [0] * len(rows)
+        for i in range(1, len(rows)):
+            starts[i] = starts[i - 1] + sizes[i - 1]
+        pair = (
+            torch.tensor(rows, dtype=torch.int32).reshape(len(rows), dim).to(device),
+            torch.tensor(starts, dtype=torch.int32).to(device),
+        )
+        _LEVEL_CACHE[key] = pair
+        if len(_LEVEL_CACHE) > _LEVEL_CACHE_MAX:
+            _LEVEL_CACHE.popitem(last=False)
+        return pair
+    spatial_i32 = value_spatial_shapes.to(device=device, dtype=torch.int32).contiguous()
+    sizes = spatial_i32.to(torch.int64).prod(dim=1)
+    starts = torch.zeros_like(sizes)
+    if sizes.numel() > 1:
+        starts[1:] = torch.cumsum(sizes[:-1], dim=0)
+    return spatial_i32, starts.to(torch.int32)
+
+
+def coord_dtype(value: torch.Tensor, loc: torch.Tensor, attn: torch.Tensor) -> torch.dtype:
+    """dtype the kernels read locations and weights in: the value dtype when all three
+    agree, else float32 (both are then upcast, which is exact for fp16/bf16)."""
+    if loc.dtype == value.dtype and attn.dtype == value.dtype:
+        return value.dtype
+    return torch.float32
+
+
+def make_desc(dim: int, value: torch.Tensor, loc: torch.Tensor, cdt: torch.dtype,
+              clamp_grid: bool, clamp_eps: float) -> _lib.MsdaDesc:
+    bsz, num_keys, num_heads, ch = value.shape
+    _, num_queries, _, num_levels, num_points, _ = loc.shape
+    d = _lib.MsdaDesc()
+    d.dim = dim
+    d.batch = bsz
+    d.num_keys = num_keys
+    d.num_heads = num_heads
+    d.channels = ch
+    d.num_queries = num_queries
+    d.num_levels = num_levels
+    d.num_points = num_points
+    d.value_dtype = _DTYPE_CODE[value.dtype]
+    d.coord_dtype = _DTYPE_CODE[cdt]
+    d.clamp_grid = 1 if clamp_grid else 0
+    d.reserved = 0
+    d.clamp_eps = float(clamp_eps)
+    return d
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def forward(dim: int, value: torch.Tensor, spatial_i32: torch.Tensor, starts_i32: torch.Tensor,
+            loc: torch.Tensor, attn: torch.Tensor, clamp_grid: bool, clamp_eps: float):
+    """Launch msda_fwd. Returns (out, value_c, loc_c, attn_c): the output and the
+    contiguous, kernel-dtype inputs it read (saved for backward)."""
+    lib = _lib.load()
+    cdt = coord_dtype(value, loc, attn)
+    value_c = value.contiguous()
+    loc_c = loc.to(dtype=cdt).contiguous()
+    attn_c = attn.to(dtype=cdt).contiguous()
+    bsz, _, num_heads, ch = value.shape
+    num_queries = loc.shape[1]
+    out = torch.empty((bsz, num_queries, num_heads * ch), device=value.device, dtype=value.dtype)
+    desc = make_desc(dim, value_c, loc_c, cdt, clamp_grid, clamp_eps)
+    with torch.cuda.device(value.device):
+        rc = lib.msda_fwd(ctypes.byref(desc), value_c.data_ptr(), spatial_i32.data_ptr(),
+                          starts_i32.data_ptr(), loc_c.data_ptr(), attn_c.data_ptr(),
+                          out.data_ptr(), _stream(value.device))
+    _lib.check(rc, "msda_fwd")
+    return out, value_c, loc_c, attn_c
+
+
+def backward(dim: int, grad_output: torch.Tensor, value_c: torch.Tensor, spatial_i32: torch.Tensor,
+             starts_i32: torch.Tensor, loc_c: torch.Tensor, attn_c: torch.Tensor,
+             clamp_grid: bool, clamp_eps: float):
+    """Launch msda_bwd. Returns (grad_value, grad_loc, grad_attn) in the kernel dtypes,
+    all freshly allocated and contiguous."""
+    lib = _lib.load()
+    grad_out = grad_output.to(dtype=value_c.dtype).contiguous()
+    grad_value = torch.empty(value_c.shape, device=value_c.device, dtype=value_c.dtype)
+    grad_loc = torch.empty(loc_c.shape, device=loc_c.device, dtype=loc_c.dtype)
+    grad_attn = torch.empty(attn_c.shape, device=attn_c.device, dtype=attn_c.dtype)
+    desc = make_desc(dim, value_c, loc_c, loc_c.dtype, clamp_grid, clamp_eps)
+    ws_bytes = int(lib.msda_bwd_workspace_bytes(ctypes.byref(desc)))
+    ws = (torch.empty(ws_bytes, device=value_c.device, dtype=torch.uint8) if ws_bytes
+          else None)
+    with torch.cuda.device(value_c.device):
+        rc = lib.msda_bwd(ctypes.byref(desc), value_c.data_ptr(), spatial_i32.data_ptr(),
+                          starts_i32.data_ptr(), loc_c.data_ptr(), attn_c.data_ptr(),
+                          grad_out.data_ptr(), grad_value.data_ptr(), grad_loc.data_ptr(),
+                          grad_attn.data_ptr(), ws.data_ptr() if ws is not None else None,
+                          ws_bytes, _stream(value_c.device))
+    _lib.check(rc, "msda_bwd")
+    return grad_value, grad_loc, grad_attn
+
+
+def fn_forward(ctx, name: str, dim: int, value, value_spatial_shapes, sampling_locations,
+               attention_weights, clamp_grid, clamp_eps) -> torch.Tensor:
+    """Body of MSDA2DFn.forward / MSDA3DFn.forward (reference triton/msda_2d.py:749-775)."""
+    validate_inputs(name, dim, value, value_spatial_shapes, sampling_locations, attention_weights)
+    spatial_i32, starts_i32 = prepare_levels(dim, value, value_spatial_shapes)
+    out, value_c, loc_c, attn_c = forward(dim, value, spatial_i32, starts_i32, sampling_locations,
+                                          attention_weights, clamp_grid, clamp_eps)
+    ctx.save_for_backward(value_c, loc_c, attn_c, spatial_i32, starts_i32)
+    ctx.clamp_grid = clamp_grid
+    ctx.clamp_eps = clamp_eps
+    ctx.in_dtypes = (value.dtype, sampling_locations.dtype, attention_weights.dtype)
+    return out
+
+
+def fn_backward(ctx, dim: int, grad_output: torch.Tensor):
+    """Body of MSDA2DFn.backward / MSDA3DFn.backward (reference triton/msda_2d.py:777-853):
+    returns (grad_value, None, grad_loc, grad_attn, None, None) in the input dtypes."""
+    value_c, loc_c, attn_c, spatial_i32, starts_i32 = ctx.saved_tensors
+    gv, gl, ga = backward(dim, grad_output, value_c, spatial_i32, starts_i32, loc_c, attn_c,
+                          ctx.clamp_grid, ctx.clamp_eps)
+    vdt, ldt, adt = ctx.in_dtypes
+    return gv.to(vdt), None, gl.to(ldt), ga.to(adt), None, None
+
+
+def run_fwd(name: str, dim: int, value, value_spatial_shapes, sampling_locations,
+            attention_weights, clamp_grid, clamp_eps) -> torch.Tensor:
+    """Forward-only entry (msda2d_fwd / msda3d_fwd)."""
+    validate_inputs(name, dim, value, value_spatial_shapes, sampling_locations, attention_weights)
+    spatial_i32, starts_i32 = prepare_levels(dim, value, value_spatial_shapes)
+    out, _, _, _ = forward(dim, value, spatial_i32, starts_i32, sampling_locations,
+                           attention_weights, clamp_grid, clamp_eps)
+    return out

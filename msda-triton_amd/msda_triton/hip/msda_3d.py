@@ -1,0 +1,77 @@
+"""3D (trilinear) multi-scale deformable attention on the gfx950 HIP kernels.
+
+Drop-in for the reference's src/msda_triton/triton/msda_3d.py: same names
+(``msda3d``, ``msda3d_fwd``, ``MSDA3DFn``), signatures, defaults, tensor contract and
+error behaviour. value (B, K, H, C); value_spatial_shapes (L, 3) as (D, H, W);
+sampling_locations (B, Q, H, L, P, 3) as (x, y, z) in [0, 1]; attention_weights
+(B, Q, H, L, P) -> (B, Q, H*C) in value's dtype, accumulated in fp32.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _core
+
+_NAME = "MSDA3D"
+_DIM = 3
+
+
+@torch.compiler.disable
+def msda3d_fwd(
+    value: torch.Tensor,
+    value_spatial_shapes: torch.Tensor,
+    sampling_locations: torch.Tensor,
+    attention_weights: torch.Tensor,
+    clamp_grid: bool = True,
+    clamp_eps: float = 1e-4,
+) -> torch.Tensor:
+    """Forward-only MSDA3D without autograd (reference triton/msda_3d.py:797-861).
+
+    Raises:
+        ValueError: inputs not on the GPU, or shape mismatch.
+        NotImplementedError: value dtype other than fp32, fp16, bf16.
+    """
+    return _core.run_fwd(_NAME, _DIM, value, value_spatial_shapes, sampling_locations,
+                         attention_weights, clamp_grid, clamp_eps)
+
+
+class MSDA3DFn(torch.autograd.Function):
+    """Autograd function for MSDA3D (reference triton/msda_3d.py:864-996).
+
+    Saves the contiguous inputs and the device level tables; backward runs one fused HIP
+    kernel for all three gradients.
+    """
+
+    @staticmethod
+    def forward(ctx, value, value_spatial_shapes, sampling_locations, attention_weights,
+                clamp_grid=True, clamp_eps=1e-4):
+        return _core.fn_forward(ctx, _NAME, _DIM, value, value_spatial_shapes,
+                                sampling_locations, attention_weights, clamp_grid, clamp_eps)
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, grad_output):
+        return _core.fn_backward(ctx, _DIM, grad_output)
+
+
+def msda3d(
+    value: torch.Tensor,
+    value_spatial_shapes: torch.Tensor,
+    sampling_locations: torch.Tensor,
+    attention_weights: torch.Tensor,
+    clamp_grid: bool = True,
+    clamp_eps: float = 1e-4,
+) -> torch.Tensor:
+    """MSDA3D with autograd; the primary training entry (reference triton/msda_3d.py:999-1050).
+
+    Raises:
+        ValueError: If inputs are not GPU tensors.
+    """
+    if not value.is_cuda:
+        raise ValueError(f"{_NAME} HIP kernel requires CUDA tensors. Got CPU tensors instead.")
+    return MSDA3DFn.apply(value, value_spatial_shapes, sampling_locations, attention_weights,
+                          clamp_grid, clamp_eps)
+
+
+__all__ = ["msda3d", "msda3d_fwd", "MSDA3DFn"]

@@ -1,0 +1,262 @@
+"""GPU parity suite shared by tests/test_msda_2d.py and tests/test_msda_3d.py.
+
+It mirrors the reference's own suites (tests/test_msda_2d.py:22-427, tests/test_msda_3d.py)
+case by case, and adds oracle parity at the north-star tolerances:
+  forward  max|out - ref| / max|ref| <= 1e-5 (fp32), <= 1e-2 (bf16/fp16 vs the fp32 oracle
+           on upcast inputs);
+  gradients (fp32) normwise max-relative <= 1e-4 against the float64 brute-force oracle
+           evaluated with the same fp32 coordinate rounding as the kernel, and against the
+           torch oracle with samples within 1e-3 px of a cell edge excluded from
+           grad_sampling_locations (there one ulp of coordinate selects another cell).
+The HIP op is reached through msda_triton (ctypes -> libmsda_hip.so); the oracle runs on
+the CPU.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import msda_triton
+from msda_triton import triton as mt_triton
+from oracle import brute, torch_ref
+from tests._util import make_inputs, max_abs, max_rel
+
+FWD_TOL_F32 = 1e-5
+FWD_TOL_HALF = 1e-2
+GRAD_TOL_F32 = 1e-4
+EDGE_TOL_PX = 1e-3
+
+
+@pytest.mark.gpu
+class ParitySuite:
+    dim = 2
+
+    @pytest.fixture(autouse=True)
+    def _setup(self) -> None:
+        if not torch.cuda.is_available():
+            pytest.skip("no GPU")
+        self.device = torch.device("cuda")
+        if self.dim == 2:
+            self.fwd, self.op, self.fn = msda_triton.msda2d_fwd, msda_triton.msda2d, mt_triton.MSDA2DFn
+        else:
+            self.fwd, self.op, self.fn = msda_triton.msda3d_fwd, msda_triton.msda3d, mt_triton.MSDA3DFn
+
+    # ------------------------------------------------------------------ helpers
+    def inputs(self, **kw):
+        return make_inputs(self.dim, **kw)
+
+    def gpu(self, *ts):
+        return [t.to(self.device) for t in ts]
+
+    def run_fwd_bwd(self, value, shapes, loc, attn, grad_out, **kw):
+        v, lo, a = [t.detach().clone().to(self.device).requires_grad_(True) for t in (value, loc, attn)]
+        out = self.op(v, shapes, lo, a, **kw)
+        out.backward(grad_out.to(self.device, out.dtype))
+        return out.detach().cpu(), v.grad.cpu(), lo.grad.cpu(), a.grad.cpu()
+
+    def check_grads(self, value, shapes, loc, attn, grad_out, gv, gl, ga, clamp_grid=True,
+                    clamp_eps=1e-4):
+        """fp32 gradients vs the brute-force oracle (fp32 coordinate rounding) and vs the
+        torch oracle with edge samples excluded from grad_loc."""
+        bv, bl, ba = brute.bwd(value, shapes, loc, attn, grad_out, clamp_grid, clamp_eps,
+                               coord_f32=True)
+        assert max_rel(gv, bv) <= GRAD_TOL_F32, f"grad_value vs brute {max_rel(gv, bv)}"
+        assert max_rel(ga, ba) <= GRAD_TOL_F32, f"grad_attn vs brute {max_rel(ga, ba)}"
+        assert max_rel(gl, bl) <= GRAD_TOL_F32, f"grad_loc vs brute {max_rel(gl, bl)}"
+        _, tv, tl, ta = torch_ref.msda_ref_grads(value, shapes, loc, attn, grad_out, clamp_grid,
+                                                 clamp_eps)
+        assert max_rel(gv, tv) <= GRAD_TOL_F32, f"grad_value vs torch {max_rel(gv, tv)}"
+        assert max_rel(ga, ta) <= GRAD_TOL_F32, f"grad_attn vs torch {max_rel(ga, ta)}"
+        keep = torch.from_numpy(~brute.edge_mask(shapes, loc, EDGE_TOL_PX, clamp_grid, clamp_eps))
+        keep = keep.unsqueeze(-1).expand_as(tl)
+        assert max_rel(gl[keep], tl[keep]) <= GRAD_TOL_F32, (
+            f"grad_loc vs torch {max_rel(gl[keep], tl[keep])} "
+            f"({int((~keep).sum()) // self.dim} edge samples excluded)")
+
+    # ------------------------------------------------------- reference-mirrored cases
+    def test_forward_pass_basic(self) -> None:
+        value, shapes, loc, attn = self.inputs()
+        ref = torch_ref.msda_ref(value, shapes, loc, attn, clamp_grid=True, clamp_eps=1e-4)
+        out = self.fwd(*self.gpu(value), shapes, *self.gpu(loc, attn), clamp_grid=True,
+                       clamp_eps=1e-4).cpu()
+        assert out.shape == ref.shape and out.dtype == torch.float32
+        assert max_abs(out, ref) < 1e-4
+        assert (out - ref).abs().mean().item() < 1e-5
+        assert max_rel(out, ref) <= FWD_TOL_F32
+        assert max_rel(out, brute.fwd(value, shapes, loc, attn)) <= FWD_TOL_F32
+
+    @pytest.mark.parametrize("cfg", [(1, 100, 4, 64, 3, 4), (4, 25, 8, 32, 2, 8),
+                                     (2, 200, 16, 16, 4, 4)])
+    def test_forward_pass_different_configs(self, cfg) -> None:
+        bs, nq, nh, dph, nl, npt = cfg
+        value, shapes, loc, attn = self.inputs(batch_size=bs, num_queries=nq, num_heads=nh,
+                                               dim_per_head=dph, num_levels=nl, num_points=npt)
+        ref = torch_ref.msda_ref(value, shapes, loc, attn)
+        out = self.fwd(*self.gpu(value), shapes, *self.gpu(loc, attn)).cpu()
+        assert max_abs(out, ref) < 1e-4
+        assert max_rel(out, ref) <= FWD_TOL_F32
+
+    def test_backward_pass_basic(self) -> None:
+        value, shapes, loc, attn = self.inputs()
+        grad_out = torch.randn(value.shape[0], loc.shape[1], value.shape[2] * value.shape[3],
+                               generator=torch.Generator().manual_seed(7))
+        out, gv, gl, ga = self.run_fwd_bwd(value, shapes, loc, attn, grad_out, clamp_grid=True,
+                                           clamp_eps=1e-4)
+        ref, tv, tl, ta = torch_ref.msda_ref_grads(value, shapes, loc, attn, grad_out)
+        # the reference suite's own absolute bounds (tests/test_msda_2d.py:207-231)
+        assert max_abs(gv, tv) < 1e-5 and (gv - tv).abs().mean() < 1e-7
+        assert max_abs(gl, tl) < 0.25 and (gl - tl).abs().mean() < 2e-5
+        assert max_abs(ga, ta) < 3e-4 and (ga - ta).abs().mean() < 1e-6
+        self.check_grads(value, shapes, loc, attn, grad_out, gv, gl, ga)
+
+    def test_fp64_not_supported(self) -> None:
+        value, shapes, loc, attn = self.inputs(batch_size=1, num_queries=10, num_heads=2,
+                                               dim_per_head=8, dtype=torch.float64)
+        with pytest.raises(NotImplementedError) as exc_info:
+            self.fwd(*self.gpu(value), shapes, *self.gpu(loc, attn))
+        assert "fp32, fp16, and bf16" in str(exc_info.value)
+        assert "float64" in str(exc_info.value)
+
+    def test_edge_case_boundary_sampling(self) -> None:
+        value, shapes, loc, attn = self.inputs(batch_size=1, num_queries=10)
+        loc[0, 0, 0, 0, 0, :] = 0.0
+        loc[0, 1, 0, 0, 0, :] = 1.0
+        loc[0, 2, 0, 0, 0, :] = torch.tensor([0.0, 1.0] if self.dim == 2 else [0.0, 1.0, 0.5])
+        ref = torch_ref.msda_ref(value, shapes, loc, attn)
+        out = self.fwd(*self.gpu(value), shapes, *self.gpu(loc, attn)).cpu()
+        assert max_abs(out, ref) < 1e-4
+        assert max_rel(out, ref) <= FWD_TOL_F32
+
+    def test_edge_case_out_of_bounds(self) -> None:
+        value, shapes, loc, attn = self.inputs(batch_size=1, num_queries=10)
+        loc[0, 0, 0, 0, 0, :] = -0.1
+        loc[0, 1, 0, 0, 0, :] = 1.1
+        ref = torch_ref.msda_ref(value, shapes, loc, attn, clamp_grid=True)
+        out = self.fwd(*self.gpu(value), shapes, *self.gpu(loc, attn), clamp_grid=True).cpu()
+        assert max_abs(out, ref) < 1e-4
+        assert max_rel(out, ref) <= FWD_TOL_F32
+        grad_out = torch.randn(1, 10, value.shape[2] * value.shape[3])
+        _, gv, gl, ga = self.run_fwd_bwd(value, shapes, loc, attn, grad_out, clamp_grid=True)
+        # a clamped coordinate passes no gradient (torch.clamp backward)
+        assert torch.all(gl[0, 0, 0, 0, 0] == 0) and torch.all(gl[0, 1, 0, 0, 0] == 0)
+        self.check_grads(value, shapes, loc, attn, grad_out, gv, gl, ga)
+
+    def test_gradient_flow_end_to_end(self) -> None:
+        value, shapes, loc, attn = self.inputs(batch_size=2, num_queries=20, num_heads=4,
+                                               dim_per_head=16)
+        v1, l1, a1 = [t.clone().requires_grad_(True) for t in (value, loc, attn)]
+        loss_ref = (torch_ref.msda_ref(v1, shapes, l1, a1) ** 2).sum()
+        loss_ref.backward()
+        v2, l2, a2 = [t.clone().to(self.device).requires_grad_(True) for t in (value, loc, attn)]
+        loss = (self.op(v2, shapes, l2, a2) ** 2).sum()
+        loss.backward()
+        assert abs(loss_ref.item() - loss.item()) < 1e-4 * max(1.0, abs(loss_ref.item()))
+        keep = torch.from_numpy(~brute.edge_mask(shapes, loc, EDGE_TOL_PX)).unsqueeze(-1)
+        keep = keep.expand_as(l1)
+        assert max_abs(v2.grad.cpu(), v1.grad) < 1e-3
+        assert max_abs(a2.grad.cpu(), a1.grad) < 1e-3
+        assert max_abs(l2.grad.cpu()[keep], l1.grad[keep]) < 1e-3
+
+    def test_no_clamp_grid(self) -> None:
+        value, shapes, loc, attn = self.inputs()
+        # widen the range so zero padding outside the level is exercised
+        loc = loc * 1.2 - 0.1
+        ref = torch_ref.msda_ref(value, shapes, loc, attn, clamp_grid=False)
+        out = self.fwd(*self.gpu(value), shapes, *self.gpu(loc, attn), clamp_grid=False).cpu()
+        assert max_abs(out, ref) < 1e-4
+        assert max_rel(out, ref) <= FWD_TOL_F32
+        grad_out = torch.randn(out.shape)
+        _, gv, gl, ga = self.run_fwd_bwd(value, shapes, loc, attn, grad_out, clamp_grid=False)
+        self.check_grads(value, shapes, loc, attn, grad_out, gv, gl, ga, clamp_grid=False)
+
+    def test_single_level(self) -> None:
+        ss = [(32, 32)] if self.dim == 2 else [(4, 5, 5)]
+        value, shapes, loc, attn = self.inputs(num_levels=1, spatial_shapes=ss)
+        ref = torch_ref.msda_ref(value, shapes, loc, attn)
+        out = self.fwd(*self.gpu(value), shapes, *self.gpu(loc, attn)).cpu()
+        assert max_abs(out, ref) < 1e-4
+        grad_out = torch.randn(out.shape)
+        _, gv, gl, ga = self.run_fwd_bwd(value, shapes, loc, attn, grad_out)
+        self.check_grads(value, shapes, loc, attn, grad_out, gv, gl, ga)
+
+    @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+    def test_half_precision(self, dtype) -> None:
+        value, shapes, loc, attn = self.inputs(batch_size=1, num_queries=50, num_heads=4,
+                                               dim_per_head=32, dtype=dtype)
+        ref = torch_ref.msda_ref(value.float(), shapes, loc.float(), attn.float())
+        out = self.fwd(*self.gpu(value), shapes, *self.gpu(loc, attn))
+        assert out.dtype == dtype and out.shape == ref.shape
+        assert max_abs(out.cpu().float(), ref) < (1e-2 if dtype == torch.float16 else 5e-2)
+        assert max_rel(out.cpu().float(), ref) <= FWD_TOL_HALF
+        grad_out = torch.randn(out.shape)
+        _, gv, gl, ga = self.run_fwd_bwd(value, shapes, loc, attn, grad_out.to(dtype))
+        for name, g in (("value", gv), ("loc", gl), ("attn", ga)):
+            assert torch.isfinite(g.float()).all(), f"grad_{name} not finite"
+        assert gv.dtype == dtype and gl.dtype == dtype and ga.dtype == dtype
+        # gradients against the fp32 oracle on the same (rounded) inputs
+        _, tv, tl, ta = torch_ref.msda_ref_grads(value.float(), shapes, loc.float(), attn.float(),
+                                                 grad_out.to(dtype).float())
+        assert max_rel(gv.float(), tv) <= FWD_TOL_HALF
+        assert max_rel(ga.float(), ta) <= FWD_TOL_HALF
+
+    # ------------------------------------------------------------- added cases
+    def test_mixed_dtype_fp32_coords(self) -> None:
+        """bf16 value with fp32 locations and weights (autocast-style inputs)."""
+        value, shapes, loc, attn = self.inputs(batch_size=1, num_queries=64)
+        vb = value.to(torch.bfloat16)
+        ref = torch_ref.msda_ref(vb.float(), shapes, loc, attn)
+        out = self.fwd(vb.to(self.device), shapes, *self.gpu(loc, attn))
+        assert out.dtype == torch.bfloat16
+        assert max_rel(out.cpu().float(), ref) <= FWD_TOL_HALF
+        grad_out = torch.randn(out.shape)
+        _, gv, gl, ga = self.run_fwd_bwd(vb, shapes, loc, attn, grad_out.to(torch.bfloat16))
+        assert gl.dtype == torch.float32 and ga.dtype == torch.float32
+        _, tv, tl, ta = torch_ref.msda_ref_grads(vb.float(), shapes, loc, attn,
+                                                 grad_out.to(torch.bfloat16).float())
+        assert max_rel(ga, ta) <= FWD_TOL_HALF
+        assert max_rel(gv.float(), tv) <= FWD_TOL_HALF
+
+    def test_gpu_resident_shapes(self) -> None:
+        value, shapes, loc, attn = self.inputs(batch_size=1)
+        a = self.fwd(*self.gpu(value), shapes, *self.gpu(loc, attn)).cpu()
+        b = self.fwd(*self.gpu(value), shapes.to(self.device, torch.int32),
+                     *self.gpu(loc, attn)).cpu()
+        assert torch.equal(a, b)
+
+    def test_non_contiguous_inputs(self) -> None:
+        value, shapes, loc, attn = self.inputs(batch_size=2, num_queries=30)
+        ref = torch_ref.msda_ref(value, shapes, loc, attn)
+        vt = value.to(self.device).transpose(0, 1).contiguous().transpose(0, 1)
+        lt = loc.to(self.device).transpose(1, 2).contiguous().transpose(1, 2)
+        at = attn.to(self.device).transpose(1, 2).contiguous().transpose(1, 2)
+        assert not vt.is_contiguous() and not lt.is_contiguous()
+        out = self.fwd(vt, shapes, lt, at).cpu()
+        assert max_rel(out, ref) <= FWD_TOL_F32
+
+    @pytest.mark.parametrize("heads,ch", [(3, 3), (5, 48), (1, 8), (2, 128)])
+    def test_odd_heads_channels(self, heads, ch) -> None:
+        """Channel counts that need narrower loads (C=3), idle lanes (C=48 -> 12 of 16 lanes)
+        and odd head counts (no shared-line head groups)."""
+        value, shapes, loc, attn = self.inputs(batch_size=2, num_queries=33, num_heads=heads,
+                                               dim_per_head=ch, num_levels=3, num_points=3)
+        ref = torch_ref.msda_ref(value, shapes, loc, attn)
+        out = self.fwd(*self.gpu(value), shapes, *self.gpu(loc, attn)).cpu()
+        assert max_rel(out, ref) <= FWD_TOL_F32
+        grad_out = torch.randn(out.shape)
+        _, gv, gl, ga = self.run_fwd_bwd(value, shapes, loc, attn, grad_out)
+        self.check_grads(value, shapes, loc, attn, grad_out, gv, gl, ga)
+
+    def test_empty_inputs(self) -> None:
+        value, shapes, loc, attn = self.inputs(batch_size=2, num_queries=0)
+        out = self.fwd(*self.gpu(value), shapes, *self.gpu(loc, attn))
+        assert out.shape == (2, 0, value.shape[2] * value.shape[3])
+        v, lo, a = [t.to(self.device).requires_grad_(True) for t in (value, loc, attn)]
+        self.op(v, shapes, lo, a).sum().backward()
+        assert torch.all(v.grad == 0)
+
+    def test_autograd_function_import_path(self) -> None:
+        value, shapes, loc, attn = self.inputs(batch_size=1, num_queries=8)
+        out = self.fn.apply(*self.gpu(value), shapes, *self.gpu(loc, attn), True, 1e-4).cpu()
+        assert max_rel(out, torch_ref.msda_ref(value, shapes, loc, attn)) <= FWD_TOL_F32
