@@ -1,0 +1,332 @@
+"""Benchmark of the MSDA hot path on one MI355X.
+
+Metric: "MSDA fwd & fwd+bwd ms + achieved HBM GB/s, 2D encoder & 3D 4-level,
+bf16". One step = one msda2d forward + backward (autograd API, preallocated grad_output) of
+the 2D Deformable-DETR encoder workload (bf16):
+B=2, H=8, C=32, L=4 levels (100x150, 50x75, 25x38, 13x19; K=19947), Q=19947, P=4.
+The 3D 4-level workload (configs[4], bf16, 10% of points within 1e-3 of a volume face) is
+timed in the same run and reported under "also".
+
+value = algorithmic bytes of fwd+bwd per step / step time, in GB/s, with inputs resident in
+HBM. Algorithmic bytes, s = element size: V = B*K*H*C*s, G = B*Q*H*L*P*2^d*C*s,
+S = B*Q*H*L*P*d*s, A = B*Q*H*L*P*s, O = B*Q*H*C*s, V' = min(V, G);
+fwd = V' + S + A + O, bwd = 2V' + 2S + 2A + O.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+       python bench.py --mode copy   (plain copy kernel of known size, for PMC calibration)
+       python bench.py --mode fwd|bwd --config c2|c5 (one entry only, for rocprofv3)
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for _p in (REPO, REPO / "msda-triton_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+import torch  # noqa: E402
+
+METRIC = "MSDA fwd & fwd+bwd ms + achieved HBM GB/s, 2D encoder & 3D 4-level, bf16"
+HBM_PEAK_GBPS = 8000.0
+
+CONFIGS = {
+    "c1": dict(dim=2, B=1, H=8, C=32, shapes=[(32, 32), (16, 16)], Q=100, P=4, dtype="fp32",
+               face_frac=0.0),
+    "c2": dict(dim=2, B=2, H=8, C=32, shapes=[(100, 150), (50, 75), (25, 38), (13, 19)],
+               Q=19947, P=4, dtype="bf16", face_frac=0.0),
+    "c3": dict(dim=2, B=8, H=8, C=32, shapes=[(100, 150), (50, 75), (25, 38), (13, 19)],
+               Q=300, P=4, dtype="bf16", face_frac=0.0),
+    "c4": dict(dim=3, B=2, H=8, C=32, shapes=[(16, 32, 32), (8, 16, 16)], Q=4096, P=4,
+               dtype="bf16", face_frac=0.0),
+    "c5": dict(dim=3, B=1, H=8, C=32, shapes=[(32, 64, 64), (16, 32, 32), (8, 16, 16), (4, 8, 8)],
+               Q=32768, P=8, dtype="bf16", face_frac=0.1),
+}
+DTYPES = {"fp32": torch.float32, "bf16": torch.bfloat16, "fp16": torch.float16}
+
+
+def num_keys(cfg) -> int:
+    k = 0
+    for s in cfg["shapes"]:
+        n = 1
+        for v in s:
+            n *= v
+        k += n
+    return k
+
+
+def algorithmic_bytes(cfg, q=None) -> dict:
+    """Compulsory HBM bytes of fwd, bwd and fwd+bwd (zero-init and workspace excluded)."""
+    s = torch.tensor([], dtype=DTYPES[cfg["dtype"]]).element_size()
+    d, B, H, C, P = cfg["dim"], cfg["B"], cfg["H"], cfg["C"], cfg["P"]
+    L, Q, K = len(cfg["shapes"]), (cfg["Q"] if q is None else q), num_keys(cfg)
+    n = B * Q * H * L * P
+    V, G = B * K * H * C * s, n * (2 ** d) * C * s
+    S, A, O = n * d * s, n * s, B * Q * H * C * s
+    Vp = min(V, G)
+    fwd = Vp + S + A + O
+    bwd = 2 * Vp + 2 * S + 2 * A + O
+    return {"fwd": fwd, "bwd": bwd, "fwd_bwd": fwd + bwd, "gathered": G}
+
+
+def make_inputs(cfg, q=None, seed=42):
+    """Seeded CPU inputs: value ~ N(0,1), locations ~ U[0,1]^d, weights = softmax over L*P of
+    N(0,1) logits; with face_frac > 0, that fraction of points gets one random coordinate
+    moved within 1e-3 of a volume face (exercises clamp_grid with clamp_eps=1e-4)."""
+    g = torch.Generator().manual_seed(seed)
+    d, B, H, C, P = cfg["dim"], cfg["B"], cfg["H"], cfg["C"], cfg["P"]
+    L, Q, K = len(cfg["shapes"]), (cfg["Q"] if q is None else q), num_keys(cfg)
+    value = torch.randn(B, K, H, C, generator=g)
+    loc = torch.rand(B, Q, H, L, P, d, generator=g)
+    logits = torch.randn(B, Q, H, L * P, generator=g)
+    if cfg["face_frac"] > 0:
+        n = B * Q * H * L * P
+        pick = torch.rand(n, generator=g) < cfg["face_frac"]
+        axis = torch.randint(0, d, (n,), generator=g)
+        side = torch.rand(n, generator=g) < 0.5
+        off = torch.rand(n, generator=g) * 1e-3
+        flat = loc.view(n, d)
+        rows = torch.nonzero(pick).squeeze(1)
+        newv = torch.where(side[rows], 1.0 - off[rows], off[rows])
+        flat[rows, axis[rows]] = newv
+    attn = logits.softmax(-1).view(B, Q, H, L, P)
+    shapes = torch.tensor(cfg["shapes"], dtype=torch.int64)
+    return value, shapes, loc, attn
+
+
+class GpuCase:
+    """Device-resident inputs of one workload plus direct entry-point timers."""
+
+    def __init__(self, cfg, device):
+        from msda_triton.hip import _core
+
+        self.core = _core
+        self.cfg = cfg
+        self.dim = cfg["dim"]
+        dt = DTYPES[cfg["dtype"]]
+        value, shapes, loc, attn = make_inputs(cfg)
+        self.shapes = shapes
+        self.value = value.to(device, dt)
+        self.loc = loc.to(device, dt)
+        self.attn = attn.to(device, dt)
+        self.levels = _core.prepare_levels(self.dim, self.value, shapes)
+        g = torch.Generator().manual_seed(7)
+        B, Q, HC = cfg["B"], cfg["Q"], cfg["H"] * cfg["C"]
+        self.grad_out = torch.randn(B, Q, HC, generator=g).to(device, dt)
+        self.op = None
+
+    def fwd(self):
+        return self.core.forward(self.dim, self.value, self.levels, self.loc, self.attn,
+                                 True, 1e-4)[0]
+
+    def bwd(self):
+        return self.core.backward(self.dim, self.grad_out, self.value, self.levels, self.loc,
+                                  self.attn, True, 1e-4)
+
+    def step(self):
+        import msda_triton
+
+        op = msda_triton.msda2d if self.dim == 2 else msda_triton.msda3d
+        v = self.value.detach().requires_grad_(True)
+        lo = self.loc.detach().requires_grad_(True)
+        a = self.attn.detach().requires_grad_(True)
+        out = op(v, self.shapes, lo, a, True, 1e-4)
+        out.backward(self.grad_out)
+        return out
+
+
+def time_events(fn, iters, warmup):
+    """Average ms per call of fn, from HIP events on the current stream (the launch stream)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / iters
+
+
+def measure_case(cfg, device, steps, warmup):
+    case = GpuCase(cfg, device)
+    byt = algorithmic_bytes(cfg)
+    fwd_ms = time_events(case.fwd, max(steps, 20), warmup)
+    bwd_ms = time_events(case.bwd, max(steps, 20), warmup)
+    # timed region: exactly `steps` autograd steps between synchronisations
+    for _ in range(warmup):
+        case.step()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        case.step()
+    e1.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    step_ms = max(e0.elapsed_time(e1) / steps, wall_ms)
+    gbps = lambda b, ms: b / (ms * 1e-3) / 1e9  # noqa: E731
+    return {
+        "config": cfg,
+        "bytes": byt,
+        "fwd_ms": fwd_ms,
+        "bwd_ms": bwd_ms,
+        "step_ms": step_ms,
+        "fwd_gbps": gbps(byt["fwd"], fwd_ms),
+        "bwd_gbps": gbps(byt["bwd"], bwd_ms),
+        "step_gbps": gbps(byt["fwd_bwd"], step_ms),
+    }
+
+
+def cpu_baseline(cfg, q_sample=None, reps=3):
+    """The oracle (torch grid_sample restatement, fp32 on upcast inputs) timed on the host
+    CPU: fwd + backward of out.sum(), on the first q_sample queries of the workload."""
+    from oracle import torch_ref
+
+    torch.set_num_threads(min(torch.get_num_threads(), len(os.sched_getaffinity(0))))
+    q_sample = cfg["Q"] if q_sample is None else min(q_sample, cfg["Q"])
+    value, shapes, loc, attn = make_inputs(cfg, q=q_sample)
+    dt = DTYPES[cfg["dtype"]]
+    value, loc, attn = (t.to(dt).float() for t in (value, loc, attn))
+
+    def run():
+        v = value.clone().requires_grad_(True)
+        lo = loc.clone().requires_grad_(True)
+        a = attn.clone().requires_grad_(True)
+        torch_ref.msda_ref(v, shapes, lo, a, True, 1e-4).sum().backward()
+
+    run()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    byt = algorithmic_bytes(cfg, q=q_sample)["fwd_bwd"]
+    return {
+        "value": round(byt / t / 1e9, 4),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"oracle/torch_ref.msda_ref fwd+bwd(out.sum()) in fp32 on bf16-rounded inputs, "
+                   f"first {q_sample} of {cfg['Q']} queries, median of {reps}; "
+                   f"{t * 1e3:.1f} ms per sample, {t * 1e3 * cfg['Q'] / q_sample:.0f} ms "
+                   f"per full step by linear scaling; CPU {platform.processor() or platform.machine()}"),
+    }
+
+
+def load_traffic(kernel: str, workload: str):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if present."""
+    f = REPO / "profiles" / "traffic.json"
+    if not f.exists():
+        return None
+    try:
+        return json.loads(f.read_text()).get(f"{kernel}:{workload}")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--mode", choices=["full", "fwd", "bwd", "step", "copy"], default="full")
+    ap.add_argument("--config", choices=sorted(CONFIGS), default="c2")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-queries", type=int, default=None)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(MSDA shards by (batch, head) with no exchange; see DESIGN.md). Use --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+
+    if args.mode == "copy":
+        n = 1 << 28  # 256 MiB read + 256 MiB written per copy
+        src = torch.ones(n, dtype=torch.uint8, device=device)
+        dst = torch.empty_like(src)
+        ms = time_events(lambda: dst.copy_(src), args.steps, args.warmup)
+        print(json.dumps({"mode": "copy", "bytes_read": n, "bytes_written": n, "ms": ms}))
+        return
+    if args.mode in ("fwd", "bwd", "step"):
+        case = GpuCase(CONFIGS[args.config], device)
+        fn = {"fwd": case.fwd, "bwd": case.bwd, "step": case.step}[args.mode]
+        ms = time_events(fn, args.steps, args.warmup)
+        print(json.dumps({"mode": args.mode, "config": args.config, "ms": ms}))
+        return
+
+    main_cfg, also_cfg = CONFIGS["c2"], CONFIGS["c5"]
+    r = measure_case(main_cfg, device, args.steps, args.warmup)
+    r5 = measure_case(also_cfg, device, args.steps, args.warmup)
+
+    # dominant launch of the step: the forward kernel, or the backward entry (its binning,
+    # scan, tile and reduce kernels, timed together on the launch stream)
+    if r["bwd_ms"] >= r["fwd_ms"]:
+        kname, kbytes, kms = ("msda_bwd (bwd_bin_kernel x2, scans, bwd_tile_kernel, "
+                              "bwd_reduce_kernel)"), r["bytes"]["bwd"], r["bwd_ms"]
+    else:
+        kname, kbytes, kms = "msda_fwd_kernel", r["bytes"]["fwd"], r["fwd_ms"]
+    achieved = kbytes / (kms * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                "traffic": load_traffic(kname, "c2_bf16"), "kernel": kname,
+                "algorithmic_bytes_per_launch": kbytes, "avg_launch_ms": round(kms, 5)}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(main_cfg, q_sample=args.cpu_queries)
+
+    def summary(x):
+        return {"fwd_ms": round(x["fwd_ms"], 5), "fwd_bwd_ms": round(x["step_ms"], 5),
+                "bwd_ms": round(x["bwd_ms"], 5), "bwd_gbps": round(x["bwd_gbps"], 2),
+                "fwd_gbps": round(x["fwd_gbps"], 2),
+                "fwd_roofline_frac": round(x["fwd_gbps"] / HBM_PEAK_GBPS, 4),
+                "fwd_bwd_gbps": round(x["step_gbps"], 2),
+                "bytes_fwd": x["bytes"]["fwd"], "bytes_fwd_bwd": x["bytes"]["fwd_bwd"]}
+
+    line = {
+        "metric": METRIC,
+        "value": round(r["step_gbps"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["step_ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "2D Deformable-DETR encoder self-attention fwd+bwd "
+                               "(BASELINE.json configs[1])",
+                   "B": 2, "H": 8, "C": 32, "levels": main_cfg["shapes"], "K": num_keys(main_cfg),
+                   "Q": main_cfg["Q"], "P": 4, "clamp_grid": True, "clamp_eps": 1e-4},
+        "c2_bf16": summary(r),
+        "also": {"c5_bf16_3d_4level": summary(r5)},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -8,10 +8,12 @@
  *
  * Tensor contract (identical to msda_triton's, reference README.md:60-68):
  *   value               (B, K, H, C)        value_dtype, contiguous
- *   spatial_shapes      (L, dim)  int32     device memory; rows are (H_l, W_l) for dim 2
- *                                           and (D_l, H_l, W_l) for dim 3
- *   level_start         (L,)      int32     device memory; exclusive prefix sum of the
- *                                           per-level sizes (row-major flattening of K)
+ *   spatial_shapes      (L, dim)  int32     rows are (H_l, W_l) for dim 2 and
+ *                                           (D_l, H_l, W_l) for dim 3; device memory for
+ *                                           msda_fwd, host memory for the backward calls
+ *   level_start         (L,)      int32     device memory (msda_fwd); exclusive prefix
+ *                                           sum of the per-level sizes (row-major
+ *                                           flattening of K)
  *   sampling_locations  (B, Q, H, L, P, dim) coord_dtype, contiguous, order (x, y[, z])
  *                                           with x along W, y along H, z along D
  *   attention_weights   (B, Q, H, L, P)      coord_dtype, contiguous
@@ -97,26 +99,31 @@ int msda_fwd(const msda_desc* desc,
              void* stream);
 
 /*
- * Bytes of device workspace msda_bwd needs for this descriptor: 0 for fp32 value,
- * B*K*H*C*4 (an fp32 grad_value accumulator) for fp16/bf16 value.
+ * Bytes of device workspace msda_bwd needs for this descriptor and these level shapes
+ * (0 when there is nothing to sample). host_spatial_shapes is a HOST array of L*dim int32
+ * laid out like spatial_shapes; the backward plans its spatial tiling from it. Returns 0
+ * and sets msda_last_error() if the descriptor or shapes are invalid.
  */
-size_t msda_bwd_workspace_bytes(const msda_desc* desc);
+size_t msda_bwd_workspace_bytes(const msda_desc* desc, const int32_t* host_spatial_shapes);
 
 /*
  * Backward of msda_fwd with respect to value, sampling_locations and attention_weights.
- * grad_value is fully overwritten (the library clears it, or its fp32 workspace, on
- * `stream` with a fill kernel), as are grad_sampling_locations and
- * grad_attention_weights. Gradients of clamped grid coordinates are zero, matching the
- * backward of torch.clamp. grad_value accumulates with device atomics, so its low-order
- * bits depend on execution order.
  *
- * Replaces the reference's MSDA2DFn.backward body (src/msda_triton/triton/msda_2d.py:778-853)
- * and MSDA3DFn.backward (src/msda_triton/triton/msda_3d.py:920-996).
+ * grad_value, grad_sampling_locations and grad_attention_weights are fully overwritten
+ * (each element exactly once, with plain stores), in the dtypes of their inputs.
+ * Gradients of clamped grid coordinates are zero, matching the backward of torch.clamp.
+ * grad_value is accumulated in fp32 in on-chip memory per spatial tile, so no device-wide
+ * atomics are used; the order of the fp32 additions within a tile is not fixed, so its
+ * low-order bits may vary between runs. `workspace` must hold
+ * msda_bwd_workspace_bytes() bytes, 256-byte aligned; it needs no initialisation.
+ *
+ * Replaces the reference's MSDA2DFn.backward body (src/msda_triton/triton/msda_2d.py:778-853,
+ * kernel _bwd_kernel_2d :263-510) and MSDA3DFn.backward (src/msda_triton/triton/msda_3d.py:
+ * 920-996, kernel _bwd_kernel :291-653).
  */
 int msda_bwd(const msda_desc* desc,
+             const int32_t* host_spatial_shapes,
              const void* value,
-             const int32_t* spatial_shapes,
-             const int32_t* level_start,
              const void* sampling_locations,
              const void* attention_weights,
              const void* grad_output,

@@ -1,9 +1,10 @@
 // msda_api.hip — extern "C" entry points declared in include/msda.h.
 //
-// Host-side work per call: validate the descriptor, pick the kernel instantiation,
-// split the batch into launches whose byte offsets fit the 32-bit buffer addressing
-// the kernels use, and enqueue everything on the caller's stream. No allocation,
-// no synchronisation, no global mutable state except the thread-local error text.
+// Host-side work per call: validate the descriptor, pick the kernel instantiation, plan
+// the backward's tile geometry from the host copy of the level shapes, split the batch
+// into launches whose byte offsets fit the 32-bit buffer addressing the kernels use, and
+// enqueue everything on the caller's stream. No allocation, no synchronisation, no global
+// mutable state except the thread-local error text.
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -36,13 +37,16 @@ const char* dtype_name(int dt) {
 }
 
 constexpr uint64_t kLim31 = 0x7FFFFFFFull;
+constexpr uint32_t kSubBatchesPerChunk = 16;  // records per chunk = 16 * S
+constexpr uint32_t kTileLdsBudget = 160 * 1024 - 256;
+constexpr int kMaxBinsLds = 8192;  // bin histogram + bases in 64 KB of LDS
 
-// Lanes per unit and vector width for C channels of `vb` bytes each.
+// Lanes per unit and per-lane vector width for one C-channel value row.
 struct Layout {
   int vec_bytes;  // bytes per lane per row
   int nvec;       // C / VEC
   int lpu_log2;   // lanes per unit = 2^lpu_log2
-  int hg_log2;    // heads per 128-byte line group
+  int hg_log2;    // heads whose rows share a 128-byte line
 };
 
 bool aligned(const void* p, int a) { return p == nullptr || ((uintptr_t)p % (uintptr_t)a) == 0; }
@@ -66,7 +70,6 @@ int choose_layout(const msda_desc* d, const void* const* ptrs, int nptr, Layout*
     return fail(MSDA_ERR_INVALID,
                 "channels per head (%d) too large: at most 64 lanes of %d bytes per head row",
                 d->channels, vb);
-  // Heads whose rows share a 128-byte line are kept on the same lanes' neighbourhood.
   int hg = 0;
   while (((row << (hg + 1)) <= 128) && (d->num_heads % (1 << (hg + 1)) == 0)) ++hg;
   out->vec_bytes = vb;
@@ -81,10 +84,9 @@ int validate(const msda_desc* d) {
   if (d->dim != 2 && d->dim != 3) return fail(MSDA_ERR_INVALID, "dim must be 2 or 3, got %d", d->dim);
   if (d->batch < 0 || d->num_keys < 0 || d->num_heads < 1 || d->channels < 1 ||
       d->num_queries < 0 || d->num_levels < 0 || d->num_points < 0)
-    return fail(MSDA_ERR_INVALID,
-                "invalid sizes: B=%d K=%lld H=%d C=%d Q=%lld L=%d P=%d", d->batch,
-                (long long)d->num_keys, d->num_heads, d->channels, (long long)d->num_queries,
-                d->num_levels, d->num_points);
+    return fail(MSDA_ERR_INVALID, "invalid sizes: B=%d K=%lld H=%d C=%d Q=%lld L=%d P=%d",
+                d->batch, (long long)d->num_keys, d->num_heads, d->channels,
+                (long long)d->num_queries, d->num_levels, d->num_points);
   if (d->value_dtype < MSDA_F32 || d->value_dtype > MSDA_BF16)
     return fail(MSDA_ERR_DTYPE, "value dtype code %d is not fp32, fp16 or bf16", d->value_dtype);
   if (d->coord_dtype != d->value_dtype && d->coord_dtype != MSDA_F32)
@@ -100,31 +102,38 @@ int validate(const msda_desc* d) {
   if (d->num_levels > msda::kMaxLevels)
     return fail(MSDA_ERR_INVALID, "at most %d levels are supported, got %d", msda::kMaxLevels,
                 d->num_levels);
-  const uint64_t lpd = (uint64_t)d->num_levels * d->num_points * d->dim;
-  if (lpd > (uint64_t)1 << 24)
-    return fail(MSDA_ERR_INVALID, "levels*points too large (%llu)", (unsigned long long)lpd);
-  // One batch must fit a launch: value bytes (and fp32 accumulator bytes) and
-  // lanes of one batch below 2^31.
+  const uint64_t lp = (uint64_t)d->num_levels * d->num_points;
+  if (lp * d->dim > ((uint64_t)1 << 24))
+    return fail(MSDA_ERR_INVALID, "levels*points too large (%llu)", (unsigned long long)lp);
+  // One batch must fit one launch: its value bytes (and the fp32 view of them), its lanes,
+  // and its backward records stay below 2^31.
   const uint64_t per_b_acc = (uint64_t)d->num_keys * d->num_heads * d->channels * 4ull;
   if (per_b_acc > kLim31)
     return fail(MSDA_ERR_INVALID,
                 "value slice of one batch is too large: K*H*C*4 = %llu bytes exceeds 2^31-1",
                 (unsigned long long)per_b_acc);
-  const uint64_t per_b_lanes = (uint64_t)d->num_queries * d->num_heads * 64ull;
-  if (per_b_lanes > kLim31)
+  const uint64_t qh = (uint64_t)d->num_queries * d->num_heads;
+  if (qh * 64ull > kLim31)
     return fail(MSDA_ERR_INVALID, "Q*H of one batch too large (%llu units)",
-                (unsigned long long)((uint64_t)d->num_queries * d->num_heads));
+                (unsigned long long)qh);
+  if (qh * lp * (1ull << d->dim) > kLim31 || (uint64_t)d->num_queries * d->num_points > kLim31)
+    return fail(MSDA_ERR_INVALID, "Q*H*L*P of one batch too large for the backward");
   return MSDA_OK;
 }
+
+int64_t min64(int64_t a, int64_t b) { return a < b ? a : b; }
 
 // Batches per launch such that every 32-bit in-kernel offset stays below 2^31.
 int64_t batches_per_launch(const msda_desc* d, const Layout& lay) {
   const uint64_t per_b_acc = (uint64_t)d->num_keys * d->num_heads * d->channels * 4ull;
-  const uint64_t per_b_lanes = ((uint64_t)d->num_queries * d->num_heads) << lay.lpu_log2;
-  uint64_t nb = (uint64_t)d->batch;
-  if (per_b_acc) nb = nb < kLim31 / per_b_acc ? nb : kLim31 / per_b_acc;
-  if (per_b_lanes) nb = nb < kLim31 / per_b_lanes ? nb : kLim31 / per_b_lanes;
-  return nb < 1 ? 1 : (int64_t)nb;
+  const uint64_t qh = (uint64_t)d->num_queries * d->num_heads;
+  const uint64_t per_b_lanes = qh << lay.lpu_log2;
+  const uint64_t per_b_rec = qh * d->num_levels * d->num_points * (1ull << d->dim);
+  int64_t nb = d->batch;
+  if (per_b_acc) nb = min64(nb, (int64_t)(kLim31 / per_b_acc));
+  if (per_b_lanes) nb = min64(nb, (int64_t)(kLim31 / per_b_lanes));
+  if (per_b_rec) nb = min64(nb, (int64_t)(kLim31 / per_b_rec));
+  return nb < 1 ? 1 : nb;
 }
 
 void fill_params(const msda_desc* d, const Layout& lay, int64_t nb, msda::Params* p) {
@@ -147,9 +156,168 @@ void fill_params(const msda_desc* d, const Layout& lay, int64_t nb, msda::Params
   p->hi_g = (float)(1.0 - d->clamp_eps);
   const uint64_t lanes = (uint64_t)p->num_units << lay.lpu_log2;
   p->nblocks = (uint32_t)((lanes + msda::kBlock - 1) / msda::kBlock);
-  const uint64_t vb = (uint64_t)d->num_keys * H * d->channels;
-  p->value_bytes = (uint32_t)(nb * vb * elem_bytes(d->value_dtype));
-  p->acc_bytes = (uint32_t)(nb * vb * 4ull);
+  p->value_bytes = (uint32_t)(nb * (uint64_t)d->num_keys * H * d->channels * elem_bytes(d->value_dtype));
+}
+
+// ---------------------------------------------------------------------------------------
+// Backward plan from the host level shapes.
+struct BwdHostPlan {
+  msda::BwdPlan pl;
+  msda::BwdSizes sz;
+  Layout lay;
+  int64_t nb;
+};
+
+int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int nptr,
+             BwdHostPlan* out) {
+  if (d->num_levels > 0 && !hs) return fail(MSDA_ERR_INVALID, "host spatial shapes are NULL");
+  memset(out, 0, sizeof(*out));
+  msda::BwdPlan& pl = out->pl;
+  int64_t total = 0;
+  for (int l = 0; l < d->num_levels; ++l) {
+    int64_t n = 1;
+    for (int k = 0; k < d->dim; ++k) {
+      const int32_t v = hs[l * d->dim + k];
+      if (v < 0) return fail(MSDA_ERR_INVALID, "spatial shape of level %d is negative", l);
+      n *= v;
+    }
+    pl.lv[l].start = (int32_t)total;
+    if (d->dim == 2) {
+      pl.lv[l].D = 1;
+      pl.lv[l].H = hs[2 * l];
+      pl.lv[l].W = hs[2 * l + 1];
+    } else {
+      pl.lv[l].D = hs[3 * l];
+      pl.lv[l].H = hs[3 * l + 1];
+      pl.lv[l].W = hs[3 * l + 2];
+    }
+    total += n;
+    if (total > (int64_t)kLim31) return fail(MSDA_ERR_INVALID, "Total number of keys exceeds int32 range");
+  }
+  if (total != d->num_keys)
+    return fail(MSDA_ERR_INVALID,
+                "value dim 1 (%lld) does not match sum of spatial shapes (%lld)",
+                (long long)d->num_keys, (long long)total);
+  // The backward's per-lane width depends on C only (never on pointer alignment), so the
+  // plan and the workspace size are the same with or without pointers.
+  const void* none[1] = {nullptr};
+  int rc = choose_layout(d, none, 0, &out->lay);
+  if (rc) return rc;
+  const Layout& lay = out->lay;
+  for (int i = 0; i < nptr; ++i)
+    if (!aligned(ptrs[i], lay.vec_bytes))
+      return fail(MSDA_ERR_INVALID, "msda_bwd: tensor pointers must be %d-byte aligned",
+                  lay.vec_bytes);
+  const int s = elem_bytes(d->value_dtype);
+  const int nc = 1 << d->dim;
+  // Tile extents and sub-batch size: start from 16x16 (2D) / 8x8x8 (3D) cells and 512
+  // records; shrink until a thread owns at most kTileMaxItems (cell, chunk) items and the
+  // staged value region, grad_out rows, sorted entries and counters fit in LDS.
+  int T[3] = {16, 16, 1};
+  if (d->dim == 3) T[0] = T[1] = T[2] = 8;
+  const uint32_t val_row = (uint32_t)(d->channels * s) + 16;  // +16 B spreads LDS banks
+  const uint32_t grow = (uint32_t)(d->channels * s);
+  uint32_t S = 512, lds = 0, vbytes = 0;
+  auto shrink = [&]() {
+    const int k = (T[2] >= T[1] && T[2] >= T[0] && T[2] > 1) ? 2 : (T[1] >= T[0] && T[1] > 1 ? 1 : 0);
+    if (T[k] <= 1) return false;
+    T[k] /= 2;
+    return true;
+  };
+  for (;;) {
+    const int cells = T[0] * T[1] * T[2];
+    const int rz = d->dim == 3 ? T[2] + 1 : 1;
+    vbytes = (((uint32_t)((T[0] + 1) * (T[1] + 1) * rz) * val_row) + 15) & ~15u;
+    lds = vbytes + S * grow + S * nc * 8u + (uint32_t)(2 * cells + 1 + msda::kTileThreads / 64) * 4u;
+    if (cells * lay.nvec > msda::kTileMaxItems * msda::kTileThreads || cells > msda::kTileThreads) {
+      if (!shrink()) return fail(MSDA_ERR_INVALID, "channels per head too large for the backward");
+      continue;
+    }
+    if (lds <= kTileLdsBudget) break;
+    if (S > 128) {
+      S /= 2;
+      continue;
+    }
+    if (!shrink()) return fail(MSDA_ERR_INVALID, "channels per head too large for the backward");
+  }
+  pl.TX = T[0];
+  pl.TY = T[1];
+  pl.TZ = T[2];
+  pl.RX = T[0] + 1;
+  pl.RY = T[1] + 1;
+  pl.RZ = d->dim == 3 ? T[2] + 1 : 1;
+  pl.cells = T[0] * T[1] * T[2];
+  pl.S = S;
+  pl.val_row_bytes = val_row;
+  pl.lds_val_bytes = vbytes;
+  pl.lds_g_bytes = S * grow;
+  pl.lds_bytes = lds;
+  int tiles = 0;
+  for (int l = 0; l < d->num_levels; ++l) {
+    msda::BwdLevel& lv = pl.lv[l];
+    lv.ntx = (lv.W + pl.TX - 1) / pl.TX;
+    lv.nty = (lv.H + pl.TY - 1) / pl.TY;
+    lv.ntz = (lv.D + pl.TZ - 1) / pl.TZ;
+    lv.tile_off = tiles;
+    const int64_t nt = (int64_t)lv.ntx * lv.nty * lv.ntz;
+    if (tiles + nt > kMaxBinsLds)
+      return fail(MSDA_ERR_INVALID,
+                  "backward: levels too large (%lld tiles per head; the binning supports %d)",
+                  (long long)(tiles + nt), kMaxBinsLds);
+    tiles += (int)nt;
+  }
+  int hg = lay.hg_log2;
+  while (hg > 0 && ((int64_t)tiles << hg) > kMaxBinsLds) --hg;
+  pl.L = d->num_levels;
+  pl.P = d->num_points;
+  pl.C = d->channels;
+  pl.H = d->num_heads;
+  pl.K = (int32_t)d->num_keys;
+  pl.Q = (uint32_t)d->num_queries;
+  pl.div_p = msda::make_fastdiv((uint32_t)(d->num_points > 0 ? d->num_points : 1));
+  pl.tiles_per_bh = tiles;
+  pl.hg_log2 = hg;
+  pl.bins = tiles << hg;
+  pl.wgpg = (int32_t)(((uint64_t)d->num_queries << hg) + msda::kBlock - 1) / msda::kBlock;
+  pl.R = kSubBatchesPerChunk * pl.S;
+  pl.lpu_log2 = lay.lpu_log2;
+  pl.nvec = lay.nvec;
+  pl.clamp = d->clamp_grid ? 1 : 0;
+  pl.lo_g = (float)(-1.0 + d->clamp_eps);
+  pl.hi_g = (float)(1.0 - d->clamp_eps);
+  int64_t nb = batches_per_launch(d, lay);
+  // the per-(tile, bin-workgroup) count matrix must stay below 2^31 entries too
+  const uint64_t per_b_counts = (uint64_t)d->num_heads * tiles * (uint64_t)pl.wgpg;
+  if (per_b_counts) nb = min64(nb, (int64_t)(kLim31 / per_b_counts));
+  if (nb < 1) nb = 1;
+  if (per_b_counts > kLim31) return fail(MSDA_ERR_INVALID, "backward count matrix too large");
+  out->nb = nb;
+  pl.groups = (int32_t)((nb * d->num_heads) >> hg);
+  pl.T = (uint32_t)pl.groups * (uint32_t)pl.bins;
+  const uint64_t records =
+      (uint64_t)nb * d->num_queries * d->num_heads * d->num_levels * d->num_points * (1u << d->dim);
+  pl.max_chunks = pl.T + (uint32_t)((records + pl.R - 1) / pl.R);
+  pl.value_bytes = (uint32_t)(nb * (uint64_t)d->num_keys * d->num_heads * d->channels * s);
+  out->sz = msda::bwd_sizes(pl, records);
+  if (!msda::bwd_supported(d->dim, d->value_dtype, d->coord_dtype, lay.vec_bytes))
+    return fail(MSDA_ERR_DTYPE, "no backward kernel for this dtype combination");
+  return MSDA_OK;
+}
+
+void carve(char* ws, const msda::BwdSizes& z, msda::BwdBuffers* bf) {
+  auto al = [](uint64_t b) { return (b + 255) & ~(uint64_t)255; };
+  char* p = ws;
+  bf->counts = reinterpret_cast<uint32_t*>(p);
+  p += al(z.counts * 4);
+  bf->scan_tmp = reinterpret_cast<uint32_t*>(p);
+  p += al(z.scan_tmp * 4);
+  bf->records = reinterpret_cast<uint32_t*>(p);
+  p += al(z.records * 4);
+  bf->tile_nch = reinterpret_cast<uint32_t*>(p);
+  p += al(z.tile_nch * 4);
+  bf->chunk_tile = reinterpret_cast<uint32_t*>(p);
+  p += al(z.chunk_tile * 4);
+  bf->scratch = reinterpret_cast<float*>(p);
 }
 
 }  // namespace
@@ -205,73 +373,70 @@ int msda_fwd(const msda_desc* d, const void* value, const int32_t* spatial_shape
   return MSDA_OK;
 }
 
-size_t msda_bwd_workspace_bytes(const msda_desc* d) {
-  if (!d || d->value_dtype == MSDA_F32) return 0;
-  if (d->batch <= 0 || d->num_keys <= 0) return 0;
-  return (size_t)d->batch * (size_t)d->num_keys * (size_t)d->num_heads * (size_t)d->channels * 4u;
+size_t msda_bwd_workspace_bytes(const msda_desc* d, const int32_t* host_spatial_shapes) {
+  g_err[0] = 0;
+  if (validate(d)) return 0;
+  const uint64_t units = (uint64_t)d->batch * d->num_queries * d->num_heads;
+  if (units == 0 || d->num_levels == 0 || d->num_points == 0) return 0;
+  BwdHostPlan hp;
+  const void* none[1] = {nullptr};
+  if (plan_bwd(d, host_spatial_shapes, none, 0, &hp)) return 0;
+  return (size_t)hp.sz.total_bytes;
 }
 
-int msda_bwd(const msda_desc* d, const void* value, const int32_t* spatial_shapes,
-             const int32_t* level_start, const void* sampling_locations,
-             const void* attention_weights, const void* grad_output, void* grad_value,
-             void* grad_sampling_locations, void* grad_attention_weights, void* workspace,
-             size_t workspace_bytes, void* stream) {
+int msda_bwd(const msda_desc* d, const int32_t* host_spatial_shapes, const void* value,
+             const void* sampling_locations, const void* attention_weights,
+             const void* grad_output, void* grad_value, void* grad_sampling_locations,
+             void* grad_attention_weights, void* workspace, size_t workspace_bytes,
+             void* stream) {
   g_err[0] = 0;
   int rc = validate(d);
   if (rc) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const int sv = elem_bytes(d->value_dtype);
   const size_t nval = (size_t)d->batch * (size_t)d->num_keys * d->num_heads * d->channels;
-  const size_t need = msda_bwd_workspace_bytes(d);
-  if (need && (!workspace || workspace_bytes < need))
-    return fail(MSDA_ERR_WORKSPACE, "msda_bwd needs %zu workspace bytes, got %zu", need,
-                workspace_bytes);
   if (nval && !grad_value) return fail(MSDA_ERR_INVALID, "msda_bwd: grad_value is NULL");
-  if (need && ((uintptr_t)workspace % 16) != 0)
-    return fail(MSDA_ERR_INVALID, "msda_bwd: workspace must be 16-byte aligned");
-  float* acc = d->value_dtype == MSDA_F32 ? static_cast<float*>(grad_value)
-                                          : static_cast<float*>(workspace);
-  hipError_t e = msda::launch_fill_zero(acc, nval, st);
-  if (e != hipSuccess) return fail(MSDA_ERR_HIP, "msda_bwd clear failed: %s", hipGetErrorString(e));
-
   const uint64_t units = (uint64_t)d->batch * d->num_queries * d->num_heads;
-  const bool has_samples = d->num_levels > 0 && d->num_points > 0;
-  if (units > 0 && has_samples) {
-    if ((d->num_keys > 0 && !value) || !sampling_locations || !attention_weights || !grad_output ||
-        !grad_sampling_locations || !grad_attention_weights || !spatial_shapes || !level_start)
-      return fail(MSDA_ERR_INVALID, "msda_bwd: required pointer is NULL");
-    const void* vptrs[2] = {value, grad_output};
-    Layout lay;
-    if ((rc = choose_layout(d, vptrs, 2, &lay))) return rc;
-    msda::LaunchFn fn =
-        msda::get_bwd_launcher(d->dim, d->value_dtype, d->coord_dtype, lay.vec_bytes);
-    if (!fn) return fail(MSDA_ERR_DTYPE, "no backward kernel for this dtype combination");
-    const int64_t nb = batches_per_launch(d, lay);
-    const int sv = elem_bytes(d->value_dtype), sc = elem_bytes(d->coord_dtype);
-    const uint64_t LP = (uint64_t)d->num_levels * d->num_points;
-    const uint64_t qh = (uint64_t)d->num_queries * d->num_heads;
-    const uint64_t kv = (uint64_t)d->num_keys * d->num_heads * d->channels;
-    for (int64_t b0 = 0; b0 < d->batch; b0 += nb) {
-      const int64_t bc = (d->batch - b0) < nb ? (d->batch - b0) : nb;
-      msda::Params p{};
-      fill_params(d, lay, bc, &p);
-      p.value = static_cast<const char*>(value) + (uint64_t)b0 * kv * sv;
-      p.loc = static_cast<const char*>(sampling_locations) + (uint64_t)b0 * qh * LP * d->dim * sc;
-      p.attn = static_cast<const char*>(attention_weights) + (uint64_t)b0 * qh * LP * sc;
-      p.grad_out = static_cast<const char*>(grad_output) + (uint64_t)b0 * qh * d->channels * sv;
-      p.grad_acc = acc + (uint64_t)b0 * kv;
-      p.grad_loc = static_cast<char*>(grad_sampling_locations) + (uint64_t)b0 * qh * LP * d->dim * sc;
-      p.grad_attn = static_cast<char*>(grad_attention_weights) + (uint64_t)b0 * qh * LP * sc;
-      p.shapes = spatial_shapes;
-      p.starts = level_start;
-      e = fn(p, st);
-      if (e != hipSuccess)
-        return fail(MSDA_ERR_HIP, "msda_bwd launch failed: %s", hipGetErrorString(e));
-    }
+  if (units == 0 || d->num_levels == 0 || d->num_points == 0) {
+    // no samples: grad_value is zero, the other gradients are empty
+    hipError_t e = msda::launch_zero_bytes(grad_value, nval * sv, st);
+    if (e != hipSuccess) return fail(MSDA_ERR_HIP, "msda_bwd clear failed: %s", hipGetErrorString(e));
+    return MSDA_OK;
   }
-  if (d->value_dtype != MSDA_F32) {
-    e = msda::launch_narrow(acc, grad_value, d->value_dtype, nval, st);
-    if (e != hipSuccess)
-      return fail(MSDA_ERR_HIP, "msda_bwd narrow failed: %s", hipGetErrorString(e));
+  if ((d->num_keys > 0 && !value) || !sampling_locations || !attention_weights || !grad_output ||
+      !grad_sampling_locations || !grad_attention_weights)
+    return fail(MSDA_ERR_INVALID, "msda_bwd: required pointer is NULL");
+  const void* vptrs[3] = {value, grad_output, grad_value};
+  BwdHostPlan hp;
+  if ((rc = plan_bwd(d, host_spatial_shapes, vptrs, 3, &hp))) return rc;
+  if (!workspace || workspace_bytes < hp.sz.total_bytes)
+    return fail(MSDA_ERR_WORKSPACE, "msda_bwd needs %llu workspace bytes, got %zu",
+                (unsigned long long)hp.sz.total_bytes, workspace_bytes);
+  if (((uintptr_t)workspace % 256) != 0)
+    return fail(MSDA_ERR_INVALID, "msda_bwd: workspace must be 256-byte aligned");
+
+  const int sc = elem_bytes(d->coord_dtype);
+  const uint64_t LP = (uint64_t)d->num_levels * d->num_points;
+  const uint64_t qh = (uint64_t)d->num_queries * d->num_heads;
+  const uint64_t kv = (uint64_t)d->num_keys * d->num_heads * d->channels;
+  msda::BwdBuffers bf{};
+  carve(static_cast<char*>(workspace), hp.sz, &bf);
+  for (int64_t b0 = 0; b0 < d->batch; b0 += hp.nb) {
+    const int64_t bc = (d->batch - b0) < hp.nb ? (d->batch - b0) : hp.nb;
+    msda::BwdPlan pl = hp.pl;
+    pl.groups = (int32_t)((bc * d->num_heads) >> pl.hg_log2);
+    pl.T = (uint32_t)pl.groups * (uint32_t)pl.bins;
+    pl.value_bytes = (uint32_t)(bc * kv * sv);
+    bf.value = static_cast<const char*>(value) + (uint64_t)b0 * kv * sv;
+    bf.loc = static_cast<const char*>(sampling_locations) + (uint64_t)b0 * qh * LP * d->dim * sc;
+    bf.attn = static_cast<const char*>(attention_weights) + (uint64_t)b0 * qh * LP * sc;
+    bf.grad_out = static_cast<const char*>(grad_output) + (uint64_t)b0 * qh * d->channels * sv;
+    bf.grad_value = static_cast<char*>(grad_value) + (uint64_t)b0 * kv * sv;
+    bf.grad_loc = static_cast<char*>(grad_sampling_locations) + (uint64_t)b0 * qh * LP * d->dim * sc;
+    bf.grad_attn = static_cast<char*>(grad_attention_weights) + (uint64_t)b0 * qh * LP * sc;
+    hipError_t e = msda::run_bwd(pl, bf, d->dim, d->value_dtype, d->coord_dtype,
+                                 hp.lay.vec_bytes, st);
+    if (e != hipSuccess) return fail(MSDA_ERR_HIP, "msda_bwd launch failed: %s", hipGetErrorString(e));
   }
   return MSDA_OK;
 }

@@ -9,22 +9,19 @@
 namespace msda {
 
 constexpr int kMaxLevels = 64;
+constexpr int kTileThreads = 1024;  // threads of the backward tile kernel
+constexpr int kTileMaxItems = 2;    // (cell, channel chunk) items owned per tile thread
 
-// Kernel parameters for one launch over a contiguous range of batches. Pointers are
+// Forward parameters for one launch over a contiguous range of batches. Pointers are
 // already offset to the first batch of the range; all in-kernel offsets are 32-bit.
 struct Params {
   const void* value;       // (Bc, K, H, C) value_dtype
   const void* loc;         // (Bc, Q, H, L, P, dim) coord_dtype
   const void* attn;        // (Bc, Q, H, L, P) coord_dtype
-  const void* grad_out;    // (Bc, Q, H*C) value_dtype (backward only)
-  void* out;               // forward: (Bc, Q, H*C) value_dtype
-  float* grad_acc;         // backward: fp32 (Bc, K, H, C) grad_value accumulator
-  void* grad_loc;          // backward: like loc
-  void* grad_attn;         // backward: like attn
-  const int32_t* shapes;   // (L, dim)
-  const int32_t* starts;   // (L,)
+  void* out;               // (Bc, Q, H*C) value_dtype
+  const int32_t* shapes;   // (L, dim) device
+  const int32_t* starts;   // (L,) device
   uint32_t value_bytes;    // bytes of value in this launch (< 2^31)
-  uint32_t acc_bytes;      // bytes of grad_acc in this launch (< 2^31)
   int32_t K, H, C, L, P;
   uint32_t Q;
   uint32_t num_units;      // Bc * Q * H
@@ -38,15 +35,82 @@ struct Params {
   uint32_t nblocks;
 };
 
-// dtype codes match msda_dtype in include/msda.h
 using LaunchFn = hipError_t (*)(const Params&, hipStream_t);
 
-// Returns the launcher for a (dim, value dtype, coord dtype, vector width) combination,
-// or nullptr if it is not instantiated. vec_bytes is VEC * sizeof(value element).
+// Forward launcher for (dim, value dtype, coord dtype, bytes per lane load), or nullptr.
 LaunchFn get_fwd_launcher(int dim, int vdt, int cdt, int vec_bytes);
-LaunchFn get_bwd_launcher(int dim, int vdt, int cdt, int vec_bytes);
 
-hipError_t launch_fill_zero(float* p, size_t n, hipStream_t s);
-hipError_t launch_narrow(const float* src, void* dst, int vdt, size_t n, hipStream_t s);
+// ---------------------------------------------------------------------------------------
+// Backward. grad_value is accumulated in key order: every (sample, corner) is binned to
+// the spatial tile of its level that owns the corner cell; one workgroup per record chunk
+// of a tile stages the tile's value rows in LDS, computes grad_sampling_locations and
+// grad_attention_weights for the samples it owns, and accumulates grad_value in LDS with
+// LDS atomics. Tiles processed by one chunk write grad_value directly; tiles split over
+// several chunks write fp32 partials that a reduce kernel sums.
+struct BwdLevel {
+  int32_t start, W, H, D;      // first row in K and extents (D = 1 in 2D)
+  int32_t ntx, nty, ntz;       // tiles along x, y, z
+  int32_t tile_off;            // index of the level's first tile within a (b, h)
+};
+
+struct BwdPlan {
+  BwdLevel lv[kMaxLevels];
+  int32_t L, P, C, H, K;
+  uint32_t Q;
+  FastDiv div_p;               // divisor P (record -> q, p)
+  int32_t TX, TY, TZ;          // owned cells per tile (TZ = 1 in 2D)
+  int32_t RX, RY, RZ;          // staged value region: tile + 1 along each axis (RZ = 1 in 2D)
+  int32_t tiles_per_bh;
+  int32_t hg_log2;
+  int32_t groups;              // (batches in launch) * H / HG
+  int32_t wgpg;                // bin-kernel workgroups per group
+  int32_t bins;                // HG * tiles_per_bh
+  uint32_t T;                  // groups * bins
+  uint32_t R;                  // records per chunk (multiple of S)
+  uint32_t S;                  // records per LDS sub-batch of the tile kernel
+  int32_t cells;               // owned cells per tile: TX * TY * TZ
+  int32_t lpu_log2, nvec;
+  int32_t clamp;
+  float lo_g, hi_g;
+  uint32_t value_bytes;
+  uint32_t val_row_bytes;      // LDS stride of a staged value row
+  uint32_t lds_val_bytes;      // bytes of the staged value region
+  uint32_t lds_g_bytes;        // bytes of the staged grad_out rows of a sub-batch
+  uint32_t lds_bytes;          // total dynamic LDS of the tile kernel
+  uint32_t max_chunks;         // grid of the tile kernel (upper bound)
+};
+
+struct BwdBuffers {
+  const void* value;
+  const void* loc;
+  const void* attn;
+  const void* grad_out;
+  void* grad_value;
+  void* grad_loc;
+  void* grad_attn;
+  uint32_t* counts;      // T*wgpg + 1: per (tile, bin-workgroup) record counts -> offsets
+  uint32_t* scan_tmp;    // scan block sums
+  uint32_t* records;     // (q*P + p) | primary << 31, grouped by tile
+  uint32_t* tile_nch;    // T + 1: chunks per tile -> chunk offsets; [T] = total chunks
+  uint32_t* chunk_tile;  // max_chunks: tile of each chunk
+  float* scratch;        // max_chunks * TX*TY*TZ*C fp32 partials of split tiles
+};
+
+struct BwdSizes {
+  uint64_t counts, scan_tmp, records, tile_nch, chunk_tile, scratch_floats;
+  uint64_t total_bytes;
+};
+
+// Workspace element counts for a plan and an upper bound on the number of records.
+BwdSizes bwd_sizes(const BwdPlan& pl, uint64_t records);
+
+// Clear `bytes` bytes of device memory with a fill kernel (no hipMemset node in graphs).
+hipError_t launch_zero_bytes(void* p, size_t bytes, hipStream_t s);
+
+// Enqueue the whole backward for one launch (batch range) on stream s.
+hipError_t run_bwd(const BwdPlan& pl, const BwdBuffers& bf, int dim, int vdt, int cdt,
+                   int vec_bytes, hipStream_t s);
+
+bool bwd_supported(int dim, int vdt, int cdt, int vec_bytes);
 
 }  // namespace msda

@@ -77,9 +77,9 @@ def load() -> ctypes.CDLL:
         lib.msda_validate.restype = ctypes.c_int
         lib.msda_fwd.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp]
         lib.msda_fwd.restype = ctypes.c_int
-        lib.msda_bwd_workspace_bytes.argtypes = [dp]
+        lib.msda_bwd_workspace_bytes.argtypes = [dp, vp]
         lib.msda_bwd_workspace_bytes.restype = ctypes.c_size_t
-        lib.msda_bwd.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, ctypes.c_size_t, vp]
+        lib.msda_bwd.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, vp, ctypes.c_size_t, vp]
         lib.msda_bwd.restype = ctypes.c_int
         version = lib.msda_abi_version()
         if version != ABI_VERSION:

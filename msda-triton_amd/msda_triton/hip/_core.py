@@ -71,21 +71,40 @@ def validate_inputs(name: str, dim: int, value: torch.Tensor, value_spatial_shap
             raise ValueError(f"{tname} must be a floating-point tensor, got {t.dtype}")
 
 
-def prepare_levels(dim: int, value: torch.Tensor,
-                   value_spatial_shapes: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """(L, dim) int32 shapes and (L,) int32 level starts on value's device.
+class Levels:
+    """Level tables of one call: (L, dim) int32 shapes and (L,) int32 starts on the device
+    (read by the forward kernel) and a host (L, dim) int32 copy of the shapes (planned from
+    by the backward). For GPU-resident shapes the host copy arrives asynchronously in pinned
+    memory; ``host()`` waits for it."""
+
+    __slots__ = ("spatial", "starts", "_host", "_event")
+
+    def __init__(self, spatial, starts, host, event=None):
+        self.spatial = spatial
+        self.starts = starts
+        self._host = host
+        self._event = event
+
+    def host(self) -> torch.Tensor:
+        if self._event is not None:
+            self._event.synchronize()
+            self._event = None
+        return self._host
+
+
+def prepare_levels(dim: int, value: torch.Tensor, value_spatial_shapes: torch.Tensor) -> Levels:
+    """Level tables on value's device, plus the host copy of the shapes.
 
     CPU-resident shapes are checked against K and the int32 range (as in
     _prepare_spatial_2d, triton/msda_2d.py:53-74) and their device copy is cached.
     GPU-resident shapes are converted on the device without a host sync and without the
-    K check (triton/msda_2d.py:76-82).
+    K check (triton/msda_2d.py:76-82); their host copy is started asynchronously.
     """
     device = value.device
     if value_spatial_shapes.device.type == "cpu":
         shapes_cpu = value_spatial_shapes.detach().to(dtype=torch.int64)
         rows = tuple(tuple(int(v) for v in r) for r in shapes_cpu.tolist())
         key = (dim, rows, device)
-        hit = _LEVEL_CACHE.get(key)
         sizes = [1] * len(rows)
         for i, r in enumerate(rows):
             for v in r:
@@ -101,26 +120,29 @@ def prepare_levels(dim: int, value: torch.Tensor,
                 f"value dim 1 ({value.size(1)}) does not match sum of spatial shapes "
                 f"({total_keys}). Ensure K = Σ({_SHAPE_NAMES[dim]}) across all levels."
             )
+        hit = _LEVEL_CACHE.get(key)
         if hit is not None:
             _LEVEL_CACHE.move_to_end(key)
             return hit
         starts = [0] * len(rows)
         for i in range(1, len(rows)):
             starts[i] = starts[i - 1] + sizes[i - 1]
-        pair = (
-            torch.tensor(rows, dtype=torch.int32).reshape(len(rows), dim).to(device),
-            torch.tensor(starts, dtype=torch.int32).to(device),
-        )
-        _LEVEL_CACHE[key] = pair
+        host = torch.tensor(rows, dtype=torch.int32).reshape(len(rows), dim).contiguous()
+        levels = Levels(host.to(device), torch.tensor(starts, dtype=torch.int32).to(device), host)
+        _LEVEL_CACHE[key] = levels
         if len(_LEVEL_CACHE) > _LEVEL_CACHE_MAX:
             _LEVEL_CACHE.popitem(last=False)
-        return pair
+        return levels
     spatial_i32 = value_spatial_shapes.to(device=device, dtype=torch.int32).contiguous()
     sizes = spatial_i32.to(torch.int64).prod(dim=1)
     starts = torch.zeros_like(sizes)
     if sizes.numel() > 1:
         starts[1:] = torch.cumsum(sizes[:-1], dim=0)
-    return spatial_i32, starts.to(torch.int32)
+    host = torch.empty(spatial_i32.shape, dtype=torch.int32, pin_memory=True)
+    host.copy_(spatial_i32, non_blocking=True)
+    event = torch.cuda.Event()
+    event.record(torch.cuda.current_stream(device))
+    return Levels(spatial_i32, starts.to(torch.int32), host, event)
 
 
 def coord_dtype(value: torch.Tensor, loc: torch.Tensor, attn: torch.Tensor) -> torch.dtype:
@@ -152,12 +174,18 @@ def make_desc(dim: int, value: torch.Tensor, loc: torch.Tensor, cdt: torch.dtype
     return d
 
 
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    """t itself if its data is 16-byte aligned (the backward's row loads need it), else an
+    aligned copy (only contiguous views with an odd storage offset are affected)."""
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def forward(dim: int, value: torch.Tensor, spatial_i32: torch.Tensor, starts_i32: torch.Tensor,
-            loc: torch.Tensor, attn: torch.Tensor, clamp_grid: bool, clamp_eps: float):
+def forward(dim: int, value: torch.Tensor, levels: Levels, loc: torch.Tensor, attn: torch.Tensor,
+            clamp_grid: bool, clamp_eps: float):
     """Launch msda_fwd. Returns (out, value_c, loc_c, attn_c): the output and the
     contiguous, kernel-dtype inputs it read (saved for backward)."""
     lib = _lib.load()
@@ -170,33 +198,34 @@ def forward(dim: int, value: torch.Tensor, spatial_i32: torch.Tensor, starts_i32
     out = torch.empty((bsz, num_queries, num_heads * ch), device=value.device, dtype=value.dtype)
     desc = make_desc(dim, value_c, loc_c, cdt, clamp_grid, clamp_eps)
     with torch.cuda.device(value.device):
-        rc = lib.msda_fwd(ctypes.byref(desc), value_c.data_ptr(), spatial_i32.data_ptr(),
-                          starts_i32.data_ptr(), loc_c.data_ptr(), attn_c.data_ptr(),
+        rc = lib.msda_fwd(ctypes.byref(desc), value_c.data_ptr(), levels.spatial.data_ptr(),
+                          levels.starts.data_ptr(), loc_c.data_ptr(), attn_c.data_ptr(),
                           out.data_ptr(), _stream(value.device))
     _lib.check(rc, "msda_fwd")
     return out, value_c, loc_c, attn_c
 
 
-def backward(dim: int, grad_output: torch.Tensor, value_c: torch.Tensor, spatial_i32: torch.Tensor,
-             starts_i32: torch.Tensor, loc_c: torch.Tensor, attn_c: torch.Tensor,
-             clamp_grid: bool, clamp_eps: float):
+def backward(dim: int, grad_output: torch.Tensor, value_c: torch.Tensor, levels: Levels,
+             loc_c: torch.Tensor, attn_c: torch.Tensor, clamp_grid: bool, clamp_eps: float):
     """Launch msda_bwd. Returns (grad_value, grad_loc, grad_attn) in the kernel dtypes,
     all freshly allocated and contiguous."""
     lib = _lib.load()
-    grad_out = grad_output.to(dtype=value_c.dtype).contiguous()
+    grad_out = _aligned(grad_output.to(dtype=value_c.dtype).contiguous())
+    value_c = _aligned(value_c)
     grad_value = torch.empty(value_c.shape, device=value_c.device, dtype=value_c.dtype)
     grad_loc = torch.empty(loc_c.shape, device=loc_c.device, dtype=loc_c.dtype)
     grad_attn = torch.empty(attn_c.shape, device=attn_c.device, dtype=attn_c.dtype)
     desc = make_desc(dim, value_c, loc_c, loc_c.dtype, clamp_grid, clamp_eps)
-    ws_bytes = int(lib.msda_bwd_workspace_bytes(ctypes.byref(desc)))
-    ws = (torch.empty(ws_bytes, device=value_c.device, dtype=torch.uint8) if ws_bytes
-          else None)
+    host = levels.host()
+    ws_bytes = int(lib.msda_bwd_workspace_bytes(ctypes.byref(desc), host.data_ptr()))
+    if ws_bytes == 0 and _lib.last_error():
+        _lib.check(_lib.MSDA_ERR_INVALID, "msda_bwd_workspace_bytes")
+    ws = torch.empty(max(ws_bytes, 1), device=value_c.device, dtype=torch.uint8)
     with torch.cuda.device(value_c.device):
-        rc = lib.msda_bwd(ctypes.byref(desc), value_c.data_ptr(), spatial_i32.data_ptr(),
-                          starts_i32.data_ptr(), loc_c.data_ptr(), attn_c.data_ptr(),
-                          grad_out.data_ptr(), grad_value.data_ptr(), grad_loc.data_ptr(),
-                          grad_attn.data_ptr(), ws.data_ptr() if ws is not None else None,
-                          ws_bytes, _stream(value_c.device))
+        rc = lib.msda_bwd(ctypes.byref(desc), host.data_ptr(), value_c.data_ptr(),
+                          loc_c.data_ptr(), attn_c.data_ptr(), grad_out.data_ptr(),
+                          grad_value.data_ptr(), grad_loc.data_ptr(), grad_attn.data_ptr(),
+                          ws.data_ptr(), ws_bytes, _stream(value_c.device))
     _lib.check(rc, "msda_bwd")
     return grad_value, grad_loc, grad_attn
 
@@ -205,10 +234,11 @@ def fn_forward(ctx, name: str, dim: int, value, value_spatial_shapes, sampling_l
                attention_weights, clamp_grid, clamp_eps) -> torch.Tensor:
     """Body of MSDA2DFn.forward / MSDA3DFn.forward (reference triton/msda_2d.py:749-775)."""
     validate_inputs(name, dim, value, value_spatial_shapes, sampling_locations, attention_weights)
-    spatial_i32, starts_i32 = prepare_levels(dim, value, value_spatial_shapes)
-    out, value_c, loc_c, attn_c = forward(dim, value, spatial_i32, starts_i32, sampling_locations,
+    levels = prepare_levels(dim, value, value_spatial_shapes)
+    out, value_c, loc_c, attn_c = forward(dim, value, levels, sampling_locations,
                                           attention_weights, clamp_grid, clamp_eps)
-    ctx.save_for_backward(value_c, loc_c, attn_c, spatial_i32, starts_i32)
+    ctx.save_for_backward(value_c, loc_c, attn_c)
+    ctx.levels = levels
     ctx.clamp_grid = clamp_grid
     ctx.clamp_eps = clamp_eps
     ctx.in_dtypes = (value.dtype, sampling_locations.dtype, attention_weights.dtype)
@@ -218,8 +248,8 @@ def fn_forward(ctx, name: str, dim: int, value, value_spatial_shapes, sampling_l
 def fn_backward(ctx, dim: int, grad_output: torch.Tensor):
     """Body of MSDA2DFn.backward / MSDA3DFn.backward (reference triton/msda_2d.py:777-853):
     returns (grad_value, None, grad_loc, grad_attn, None, None) in the input dtypes."""
-    value_c, loc_c, attn_c, spatial_i32, starts_i32 = ctx.saved_tensors
-    gv, gl, ga = backward(dim, grad_output, value_c, spatial_i32, starts_i32, loc_c, attn_c,
+    value_c, loc_c, attn_c = ctx.saved_tensors
+    gv, gl, ga = backward(dim, grad_output, value_c, ctx.levels, loc_c, attn_c,
                           ctx.clamp_grid, ctx.clamp_eps)
     vdt, ldt, adt = ctx.in_dtypes
     return gv.to(vdt), None, gl.to(ldt), ga.to(adt), None, None
@@ -229,7 +259,7 @@ def run_fwd(name: str, dim: int, value, value_spatial_shapes, sampling_locations
             attention_weights, clamp_grid, clamp_eps) -> torch.Tensor:
     """Forward-only entry (msda2d_fwd / msda3d_fwd)."""
     validate_inputs(name, dim, value, value_spatial_shapes, sampling_locations, attention_weights)
-    spatial_i32, starts_i32 = prepare_levels(dim, value, value_spatial_shapes)
-    out, _, _, _ = forward(dim, value, spatial_i32, starts_i32, sampling_locations,
-                           attention_weights, clamp_grid, clamp_eps)
+    levels = prepare_levels(dim, value, value_spatial_shapes)
+    out, _, _, _ = forward(dim, value, levels, sampling_locations, attention_weights, clamp_grid,
+                           clamp_eps)
     return out
