@@ -367,6 +367,7 @@ int msda_fwd(const msda_desc* d, const void* value, const int32_t* spatial_shape
     p.out = static_cast<char*>(output) + (uint64_t)b0 * qh * d->channels * sv;
     p.shapes = spatial_shapes;
     p.starts = level_start;
+    p.coords_aligned = aligned(p.loc, 16) && aligned(p.attn, 16);
     hipError_t e = fn(p, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(MSDA_ERR_HIP, "msda_fwd launch failed: %s", hipGetErrorString(e));
   }

@@ -59,14 +59,73 @@ __device__ inline void stage_levels(const Params& p, Level* s_lvl) {
 
 }  // namespace
 
+// Raw storage for N elements of EC read with the widest aligned loads.
+template <typename EC, int N>
+struct CoordBlock {
+  static constexpr int kBytes = N * EC::kBytes;
+  static constexpr int kDwords = (kBytes + 3) / 4;
+  uint32_t d[kDwords];
+};
+
+template <typename EC, int N>
+__device__ inline void load_block(CoordBlock<EC, N>& b, const typename EC::T* p) {
+  constexpr int B = CoordBlock<EC, N>::kBytes;
+  if constexpr (B % 16 == 0) {
+#pragma unroll
+    for (int i = 0; i < B / 16; ++i) {
+      const u32x4 v = reinterpret_cast<const u32x4*>(p)[i];
+      b.d[4 * i] = v[0];
+      b.d[4 * i + 1] = v[1];
+      b.d[4 * i + 2] = v[2];
+      b.d[4 * i + 3] = v[3];
+    }
+  } else if constexpr (B % 8 == 0) {
+#pragma unroll
+    for (int i = 0; i < B / 8; ++i) {
+      const u32x2 v = reinterpret_cast<const u32x2*>(p)[i];
+      b.d[2 * i] = v[0];
+      b.d[2 * i + 1] = v[1];
+    }
+  } else if constexpr (B % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < B / 4; ++i) b.d[i] = reinterpret_cast<const uint32_t*>(p)[i];
+  } else {
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(p);
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      if (i & 1) b.d[i / 2] |= (uint32_t)h[i] << 16;
+      else b.d[i / 2] = h[i];
+    }
+  }
+}
+
+// Element i of a block as fp32.
+template <typename EC, int N>
+__device__ inline float block_elem(const CoordBlock<EC, N>& b, int i) {
+  if constexpr (EC::kBytes == 4) {
+    return __builtin_bit_cast(float, b.d[i]);
+  } else {
+    const uint32_t u = b.d[i / 2];
+    if constexpr (__is_same(EC, BF16)) return (i & 1) ? bf16hi(u) : bf16lo(u);
+    else return (i & 1) ? f16hi(u) : f16lo(u);
+  }
+}
+
 // Replaces the reference's _fwd_kernel_2d (src/msda_triton/triton/msda_2d.py:85-260) and
 // _fwd_kernel (src/msda_triton/triton/msda_3d.py:80-288). Writes (B, Q, H*C) in the value
 // dtype directly instead of an fp32 (B*H, Q, C) scratch plus permute (msda_2d.py:649-651).
-template <int DIM, typename EV, typename EC, int VEC>
+//
+// PT > 0: the number of points per level is a compile-time constant. Each level's PT*DIM
+// coordinates and PT weights are fetched as one contiguous block per lane, the next
+// level's block is fetched while this level's corner rows are in flight, and all corner
+// rows of a level (in batches of SB samples) are issued before any is consumed; the
+// in-order completion of vector loads then never makes a coordinate load wait behind a
+// row gather. PT == 0 handles any P with per-sample loads.
+template <int DIM, typename EV, typename EC, int VEC, int PT>
 __global__ __launch_bounds__(kBlock) void msda_fwd_kernel(const Params p) {
   constexpr int VB = VEC * EV::kBytes;
   constexpr int NC = 1 << DIM;
-  constexpr int SB = DIM == 2 ? 4 : 2;  // samples per load batch: 16 corner rows in flight
+  constexpr int SB = PT > 0 ? (DIM == 2 ? (PT < 4 ? PT : 4) : (PT < 2 ? PT : 2)) : (DIM == 2 ? 4 : 2);
   typedef typename EC::T TC;
   __shared__ Level s_lvl[kMaxLevels];
   stage_levels<DIM>(p, s_lvl);
@@ -88,35 +147,51 @@ __global__ __launch_bounds__(kBlock) void msda_fwd_kernel(const Params p) {
 #pragma unroll
   for (int i = 0; i < VEC; ++i) acc[i] = 0.0f;
 
-  for (int l = 0; l < p.L; ++l) {
-    const Level lv = s_lvl[l];
-    const uint32_t W = (uint32_t)lv.W, HW = (uint32_t)lv.W * (uint32_t)lv.H;
-    for (int p0 = 0; p0 < p.P; p0 += SB) {
-      RawVec<VB> raw[SB][NC];
+  if constexpr (PT > 0) {
+    // Software pipeline over batches of SB samples (all levels, in order): the batch's
+    // coordinates and weights were fetched during the previous iteration.
+    constexpr int BPL = PT / SB;  // batches per level
+    CoordBlock<EC, SB * DIM> lb;
+    CoordBlock<EC, SB> ab;
+    const int nbatch = p.L * BPL;
+    if (nbatch > 0) {
+      load_block<EC, SB * DIM>(lb, locp);
+      load_block<EC, SB>(ab, attp);
+    }
+#pragma unroll 1
+    for (int bi = 0; bi < nbatch; ++bi) {
+      const Level lv = s_lvl[bi / BPL];
+      const uint32_t W = (uint32_t)lv.W, HW = (uint32_t)lv.W * (uint32_t)lv.H;
+      uint32_t off[SB][NC];
       float cw[SB][NC];
 #pragma unroll
       for (int k = 0; k < SB; ++k) {
-        const int s = l * p.P + p0 + k;
-        if (p0 + k < p.P) {
-          const float a = (float)attp[s];
-          const Sample<DIM> sm = make_sample<DIM>(locp + s * DIM, lv, p.clamp, p.lo_g, p.hi_g);
-          uint32_t row0 = (uint32_t)lv.start + (uint32_t)sm.ay.i0 * W + (uint32_t)sm.ax.i0;
-          if constexpr (DIM == 3) row0 += (uint32_t)sm.az.i0 * HW;
-          const uint32_t off0 = vbase + row0 * rs;
-#pragma unroll
-          for (int c = 0; c < NC; ++c) {
-            const uint32_t dr = ((c & 1) ? 1u : 0u) + ((c & 2) ? W : 0u) +
-                                ((DIM == 3 && (c & 4)) ? HW : 0u);
-            raw[k][c] = buf_load<VB>(rv, corner_valid<DIM>(c, sm) ? off0 + dr * rs : kOobOffset);
-            cw[k][c] = corner_weight<DIM>(c, sm) * a;
-          }
-        } else {
-#pragma unroll
-          for (int c = 0; c < NC; ++c) {
-            raw[k][c] = buf_load<VB>(rv, kOobOffset);
-            cw[k][c] = 0.0f;
-          }
+        Sample<DIM> sm;
+        sm.ax = make_axis(block_elem(lb, k * DIM + 0), (float)lv.W, lv.W, p.clamp, p.lo_g, p.hi_g);
+        sm.ay = make_axis(block_elem(lb, k * DIM + 1), (float)lv.H, lv.H, p.clamp, p.lo_g, p.hi_g);
+        uint32_t row0 = (uint32_t)lv.start + (uint32_t)sm.ay.i0 * W + (uint32_t)sm.ax.i0;
+        if constexpr (DIM == 3) {
+          sm.az = make_axis(block_elem(lb, k * DIM + 2), (float)lv.D, lv.D, p.clamp, p.lo_g, p.hi_g);
+          row0 += (uint32_t)sm.az.i0 * HW;
         }
+        const float a = block_elem(ab, k);
+        const uint32_t off0 = vbase + row0 * rs;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const uint32_t dr = ((c & 1) ? 1u : 0u) + ((c & 2) ? W : 0u) + ((DIM == 3 && (c & 4)) ? HW : 0u);
+          off[k][c] = corner_valid<DIM>(c, sm) ? off0 + dr * rs : kOobOffset;
+          cw[k][c] = corner_weight<DIM>(c, sm) * a;
+        }
+      }
+      RawVec<VB> raw[SB][NC];
+#pragma unroll
+      for (int k = 0; k < SB; ++k)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) raw[k][c] = buf_load<VB>(rv, off[k][c]);
+      if (bi + 1 < nbatch) {
+        // next batch's coordinates and weights, queued behind this batch's rows
+        load_block<EC, SB * DIM>(lb, locp + (bi + 1) * (SB * DIM));
+        load_block<EC, SB>(ab, attp + (bi + 1) * SB);
       }
 #pragma unroll
       for (int k = 0; k < SB; ++k) {
@@ -129,6 +204,46 @@ __global__ __launch_bounds__(kBlock) void msda_fwd_kernel(const Params p) {
         }
       }
     }
+  } else {
+    for (int l = 0; l < p.L; ++l) {
+      const Level lv = s_lvl[l];
+      const uint32_t W = (uint32_t)lv.W, HW = (uint32_t)lv.W * (uint32_t)lv.H;
+      for (int p0 = 0; p0 < p.P; p0 += SB) {
+        RawVec<VB> raw[SB][NC];
+        float cw[SB][NC];
+#pragma unroll
+        for (int k = 0; k < SB; ++k) {
+          const int s = l * p.P + p0 + k;
+          const bool live = p0 + k < p.P;
+          const float a = live ? (float)attp[s] : 0.0f;
+          const Sample<DIM> sm =
+              make_sample<DIM>(locp + (live ? s : 0) * DIM, lv, p.clamp, p.lo_g, p.hi_g);
+          uint32_t row0 = (uint32_t)lv.start + (uint32_t)sm.ay.i0 * W + (uint32_t)sm.ax.i0;
+          if constexpr (DIM == 3) row0 += (uint32_t)sm.az.i0 * HW;
+          const uint32_t off0 = vbase + row0 * rs;
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            const uint32_t dr = ((c & 1) ? 1u : 0u) + ((c & 2) ? W : 0u) +
+                                ((DIM == 3 && (c & 4)) ? HW : 0u);
+            raw[k][c] = buf_load<VB>(rv, (live && corner_valid<DIM>(c, sm)) ? off0 + dr * rs : kOobOffset);
+            cw[k][c] = corner_weight<DIM>(c, sm) * a;
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < SB; ++k) {
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            float v[VEC];
+            widen<EV, VEC>(raw[k][c], v);
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) acc[i] = __builtin_fmaf(cw[k][c], v[i], acc[i]);
+          }
+        }
+        // keep the compiler from hoisting the next batch's row loads above these FMAs,
+        // which would multiply the live row registers and cut occupancy
+        asm volatile("" ::: "memory");
+      }
+    }
   }
   typename EV::T* outp = static_cast<typename EV::T*>(p.out) + (size_t)u.bqh * p.C + u.lane * VEC;
   store_vec<EV, VEC>(outp, acc);
@@ -136,7 +251,13 @@ __global__ __launch_bounds__(kBlock) void msda_fwd_kernel(const Params p) {
 
 template <int DIM, typename EV, typename EC, int VEC>
 static hipError_t launch_fwd(const Params& p, hipStream_t s) {
-  hipLaunchKernelGGL((msda_fwd_kernel<DIM, EV, EC, VEC>), dim3(p.nblocks), dim3(kBlock), 0, s, p);
+  // compile-time point counts for the common 4 and 8 points per level
+  if (p.P == 4 && p.coords_aligned)
+    hipLaunchKernelGGL((msda_fwd_kernel<DIM, EV, EC, VEC, 4>), dim3(p.nblocks), dim3(kBlock), 0, s, p);
+  else if (p.P == 8 && p.coords_aligned)
+    hipLaunchKernelGGL((msda_fwd_kernel<DIM, EV, EC, VEC, 8>), dim3(p.nblocks), dim3(kBlock), 0, s, p);
+  else
+    hipLaunchKernelGGL((msda_fwd_kernel<DIM, EV, EC, VEC, 0>), dim3(p.nblocks), dim3(kBlock), 0, s, p);
   return hipGetLastError();
 }
 

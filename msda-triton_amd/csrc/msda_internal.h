@@ -33,6 +33,7 @@ struct Params {
   int32_t clamp;
   float lo_g, hi_g;        // grid clamp bounds as fp32
   uint32_t nblocks;
+  int32_t coords_aligned;  // loc and attn are 16-byte aligned: per-level block loads allowed
 };
 
 using LaunchFn = hipError_t (*)(const Params&, hipStream_t);

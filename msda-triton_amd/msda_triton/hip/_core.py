@@ -190,9 +190,9 @@ def forward(dim: int, value: torch.Tensor, levels: Levels, loc: torch.Tensor, at
     contiguous, kernel-dtype inputs it read (saved for backward)."""
     lib = _lib.load()
     cdt = coord_dtype(value, loc, attn)
-    value_c = value.contiguous()
-    loc_c = loc.to(dtype=cdt).contiguous()
-    attn_c = attn.to(dtype=cdt).contiguous()
+    value_c = _aligned(value.contiguous())
+    loc_c = _aligned(loc.to(dtype=cdt).contiguous())
+    attn_c = _aligned(attn.to(dtype=cdt).contiguous())
     bsz, _, num_heads, ch = value.shape
     num_queries = loc.shape[1]
     out = torch.empty((bsz, num_queries, num_heads * ch), device=value.device, dtype=value.dtype)
