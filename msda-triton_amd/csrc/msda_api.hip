@@ -210,14 +210,21 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
                   lay.vec_bytes);
   const int s = elem_bytes(d->value_dtype);
   const int nc = 1 << d->dim;
+  const int rw = d->dim + 2;  // words per record
+  if ((uint64_t)d->num_queries * d->num_points > (uint64_t)msda::kRecIdMask)
+    return fail(MSDA_ERR_INVALID,
+                "backward supports Q*P up to 2^27 per launch, got Q=%lld P=%d",
+                (long long)d->num_queries, d->num_points);
   // Tile extents and sub-batch size: start from 16x16 (2D) / 8x8x8 (3D) cells and 512
-  // records; shrink until a thread owns at most kTileMaxItems (cell, chunk) items and the
-  // staged value region, grad_out rows, sorted entries and counters fit in LDS.
+  // records; shrink until a thread owns at most kTileMaxItems (region cell, chunk) items,
+  // the region has at most kTileThreads cells, and the staged value region, grad_out rows,
+  // records, sorted entries and counters fit in LDS.
   int T[3] = {16, 16, 1};
   if (d->dim == 3) T[0] = T[1] = T[2] = 8;
   const uint32_t val_row = (uint32_t)(d->channels * s) + 16;  // +16 B spreads LDS banks
   const uint32_t grow = (uint32_t)(d->channels * s);
   uint32_t S = 512, lds = 0, vbytes = 0;
+  int rcells = 0;
   auto shrink = [&]() {
     const int k = (T[2] >= T[1] && T[2] >= T[0] && T[2] > 1) ? 2 : (T[1] >= T[0] && T[1] > 1 ? 1 : 0);
     if (T[k] <= 1) return false;
@@ -225,11 +232,12 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
     return true;
   };
   for (;;) {
-    const int cells = T[0] * T[1] * T[2];
     const int rz = d->dim == 3 ? T[2] + 1 : 1;
-    vbytes = (((uint32_t)((T[0] + 1) * (T[1] + 1) * rz) * val_row) + 15) & ~15u;
-    lds = vbytes + S * grow + S * nc * 8u + (uint32_t)(2 * cells + 1 + msda::kTileThreads / 64) * 4u;
-    if (cells * lay.nvec > msda::kTileMaxItems * msda::kTileThreads || cells > msda::kTileThreads) {
+    rcells = (T[0] + 1) * (T[1] + 1) * rz;
+    vbytes = (((uint32_t)rcells * val_row) + 15) & ~15u;
+    lds = vbytes + S * grow + S * nc * 8u + S * rw * 4u +
+          (uint32_t)(2 * rcells + 1 + msda::kTileThreads / 64) * 4u;
+    if (rcells * lay.nvec > msda::kTileMaxItems * msda::kTileThreads || rcells > msda::kTileThreads) {
       if (!shrink()) return fail(MSDA_ERR_INVALID, "channels per head too large for the backward");
       continue;
     }
@@ -247,6 +255,7 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
   pl.RY = T[1] + 1;
   pl.RZ = d->dim == 3 ? T[2] + 1 : 1;
   pl.cells = T[0] * T[1] * T[2];
+  pl.rcells = rcells;
   pl.S = S;
   pl.val_row_bytes = val_row;
   pl.lds_val_bytes = vbytes;
@@ -286,19 +295,20 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
   pl.lo_g = (float)(-1.0 + d->clamp_eps);
   pl.hi_g = (float)(1.0 - d->clamp_eps);
   int64_t nb = batches_per_launch(d, lay);
-  // the per-(tile, bin-workgroup) count matrix must stay below 2^31 entries too
+  // the per-(bin workgroup, tile) count matrix must stay below 2^31 entries too
   const uint64_t per_b_counts = (uint64_t)d->num_heads * tiles * (uint64_t)pl.wgpg;
+  if (per_b_counts > kLim31) return fail(MSDA_ERR_INVALID, "backward count matrix too large");
   if (per_b_counts) nb = min64(nb, (int64_t)(kLim31 / per_b_counts));
   if (nb < 1) nb = 1;
-  if (per_b_counts > kLim31) return fail(MSDA_ERR_INVALID, "backward count matrix too large");
   out->nb = nb;
   pl.groups = (int32_t)((nb * d->num_heads) >> hg);
   pl.T = (uint32_t)pl.groups * (uint32_t)pl.bins;
-  const uint64_t records =
-      (uint64_t)nb * d->num_queries * d->num_heads * d->num_levels * d->num_points * (1u << d->dim);
-  pl.max_chunks = pl.T + (uint32_t)((records + pl.R - 1) / pl.R);
+  const uint64_t samples =
+      (uint64_t)nb * d->num_queries * d->num_heads * d->num_levels * d->num_points;
+  pl.max_chunks = pl.T + (uint32_t)((samples + pl.R - 1) / pl.R);
+  pl.grid_chunks = (pl.max_chunks + msda::kXcds - 1) / msda::kXcds * msda::kXcds;
   pl.value_bytes = (uint32_t)(nb * (uint64_t)d->num_keys * d->num_heads * d->channels * s);
-  out->sz = msda::bwd_sizes(pl, records);
+  out->sz = msda::bwd_sizes(pl, samples, d->dim);
   if (!msda::bwd_supported(d->dim, d->value_dtype, d->coord_dtype, lay.vec_bytes))
     return fail(MSDA_ERR_DTYPE, "no backward kernel for this dtype combination");
   return MSDA_OK;
@@ -309,14 +319,14 @@ void carve(char* ws, const msda::BwdSizes& z, msda::BwdBuffers* bf) {
   char* p = ws;
   bf->counts = reinterpret_cast<uint32_t*>(p);
   p += al(z.counts * 4);
-  bf->scan_tmp = reinterpret_cast<uint32_t*>(p);
-  p += al(z.scan_tmp * 4);
-  bf->records = reinterpret_cast<uint32_t*>(p);
-  p += al(z.records * 4);
-  bf->tile_nch = reinterpret_cast<uint32_t*>(p);
-  p += al(z.tile_nch * 4);
+  bf->bin_start = reinterpret_cast<uint32_t*>(p);
+  p += al(z.bin_start * 4);
+  bf->chunk_off = reinterpret_cast<uint32_t*>(p);
+  p += al(z.chunk_off * 4);
   bf->chunk_tile = reinterpret_cast<uint32_t*>(p);
   p += al(z.chunk_tile * 4);
+  bf->records = reinterpret_cast<uint32_t*>(p);
+  p += al(z.record_words * 4);
   bf->scratch = reinterpret_cast<float*>(p);
 }
 

@@ -42,12 +42,22 @@ using LaunchFn = hipError_t (*)(const Params&, hipStream_t);
 LaunchFn get_fwd_launcher(int dim, int vdt, int cdt, int vec_bytes);
 
 // ---------------------------------------------------------------------------------------
-// Backward. grad_value is accumulated in key order: every (sample, corner) is binned to
-// the spatial tile of its level that owns the corner cell; one workgroup per record chunk
-// of a tile stages the tile's value rows in LDS, computes grad_sampling_locations and
-// grad_attention_weights for the samples it owns, and accumulates grad_value in LDS with
-// LDS atomics. Tiles processed by one chunk write grad_value directly; tiles split over
-// several chunks write fp32 partials that a reduce kernel sums.
+// Backward. grad_value is accumulated in key order. Every sample with a valid corner is
+// binned to the spatial tile of its level that owns its lowest corner; the tile's value
+// region (the tile plus a one-cell halo on the high side of each axis) then holds all of
+// the sample's corners. One workgroup per chunk of a tile's records stages that region
+// in LDS, computes grad_sampling_locations and grad_attention_weights of its samples
+// from the staged rows, and accumulates grad_value for the region in fp32 registers of
+// the cell owners (records are sorted by cell in LDS with integer LDS atomics). Interior
+// cells of a tile processed by one chunk are written directly; edge cells, halo cells and
+// split tiles go through fp32 partials that a fold kernel sums, in a fixed order, into
+// the cells' final values.
+constexpr uint32_t kRecIdBits = 27;                     // record id = q * P + p
+constexpr uint32_t kRecIdMask = (1u << kRecIdBits) - 1u;
+constexpr uint32_t kRecPassX = 1u << 27;                // grid clamp inactive on x / y / z
+constexpr uint32_t kRecPassY = 1u << 28;
+constexpr uint32_t kRecPassZ = 1u << 29;
+
 struct BwdLevel {
   int32_t start, W, H, D;      // first row in K and extents (D = 1 in 2D)
   int32_t ntx, nty, ntz;       // tiles along x, y, z
@@ -58,18 +68,19 @@ struct BwdPlan {
   BwdLevel lv[kMaxLevels];
   int32_t L, P, C, H, K;
   uint32_t Q;
-  FastDiv div_p;               // divisor P (record -> q, p)
+  FastDiv div_p;               // divisor P (record id -> q, p)
   int32_t TX, TY, TZ;          // owned cells per tile (TZ = 1 in 2D)
-  int32_t RX, RY, RZ;          // staged value region: tile + 1 along each axis (RZ = 1 in 2D)
+  int32_t RX, RY, RZ;          // region: tile + 1 along each axis (RZ = 1 in 2D)
+  int32_t cells;               // owned cells per tile: TX * TY * TZ
+  int32_t rcells;              // region cells per tile: RX * RY * RZ (<= kTileThreads)
   int32_t tiles_per_bh;
   int32_t hg_log2;
   int32_t groups;              // (batches in launch) * H / HG
   int32_t wgpg;                // bin-kernel workgroups per group
   int32_t bins;                // HG * tiles_per_bh
-  uint32_t T;                  // groups * bins
+  uint32_t T;                  // groups * bins: tiles of this launch
   uint32_t R;                  // records per chunk (multiple of S)
   uint32_t S;                  // records per LDS sub-batch of the tile kernel
-  int32_t cells;               // owned cells per tile: TX * TY * TZ
   int32_t lpu_log2, nvec;
   int32_t clamp;
   float lo_g, hi_g;
@@ -78,7 +89,8 @@ struct BwdPlan {
   uint32_t lds_val_bytes;      // bytes of the staged value region
   uint32_t lds_g_bytes;        // bytes of the staged grad_out rows of a sub-batch
   uint32_t lds_bytes;          // total dynamic LDS of the tile kernel
-  uint32_t max_chunks;         // grid of the tile kernel (upper bound)
+  uint32_t max_chunks;         // upper bound of the chunk count
+  uint32_t grid_chunks;        // tile-kernel grid: max_chunks rounded up to 8 (one per XCD)
 };
 
 struct BwdBuffers {
@@ -89,21 +101,21 @@ struct BwdBuffers {
   void* grad_value;
   void* grad_loc;
   void* grad_attn;
-  uint32_t* counts;      // T*wgpg + 1: per (tile, bin-workgroup) record counts -> offsets
-  uint32_t* scan_tmp;    // scan block sums
-  uint32_t* records;     // (q*P + p) | primary << 31, grouped by tile
-  uint32_t* tile_nch;    // T + 1: chunks per tile -> chunk offsets; [T] = total chunks
+  uint32_t* counts;      // groups * wgpg * bins: per-(bin workgroup, bin) counts -> offsets
+  uint32_t* bin_start;   // T + 1: record totals -> first record of each tile
+  uint32_t* chunk_off;   // T + 1: first chunk of each tile; [T] = number of chunks
   uint32_t* chunk_tile;  // max_chunks: tile of each chunk
-  float* scratch;        // max_chunks * TX*TY*TZ*C fp32 partials of split tiles
+  uint32_t* records;     // (DIM + 2) words per record: id | flags, u_x, u_y[, u_z], attn
+  float* scratch;        // max_chunks * rcells * C fp32 partials
 };
 
 struct BwdSizes {
-  uint64_t counts, scan_tmp, records, tile_nch, chunk_tile, scratch_floats;
+  uint64_t counts, bin_start, chunk_off, chunk_tile, record_words, scratch_floats;
   uint64_t total_bytes;
 };
 
-// Workspace element counts for a plan and an upper bound on the number of records.
-BwdSizes bwd_sizes(const BwdPlan& pl, uint64_t records);
+// Workspace element counts for a plan, `samples` samples and dimension dim.
+BwdSizes bwd_sizes(const BwdPlan& pl, uint64_t samples, int dim);
 
 // Clear `bytes` bytes of device memory with a fill kernel (no hipMemset node in graphs).
 hipError_t launch_zero_bytes(void* p, size_t bytes, hipStream_t s);

@@ -24,21 +24,43 @@ struct Axis {
   bool pass;    // gradient passes the grid clamp (backward mask of torch.clamp)
 };
 
-__device__ inline Axis make_axis(float loc, float size_f, int size_i, int clamp, float lo,
-                                 float hi) {
+// Tile (along one axis, extent T cells) that owns a sample's lowest valid corner; the
+// sample must have a valid corner on this axis (i0 >= -1). Its corners i0 and i0 + 1
+// then lie in [tile * T - 1, tile * T + T]: the tile or its one-cell high-side halo.
+__device__ inline int anchor_tile(const Axis& a, int T) { return (a.i0 < 0 ? 0 : a.i0) / T; }
+
+// Pixel coordinate u of one location component; *pass is false where the grid clamp
+// was active.
+__device__ inline float grid_to_u(float loc, float size_f, int clamp, float lo, float hi,
+                                  bool* pass) {
+#pragma clang fp contract(off)
+  float g = 2.0f * loc - 1.0f;
+  *pass = !clamp || (g >= lo && g <= hi);
+  if (clamp) g = fminf(fmaxf(g, lo), hi);
+  return ((g + 1.0f) * size_f - 1.0f) * 0.5f;
+}
+
+// Corner indices, weights and validity from a pixel coordinate. Every kernel derives an
+// axis through this function, so a coordinate stored by one kernel and expanded by
+// another selects the same corners with the same weights.
+__device__ inline Axis axis_from_u(float u, int size_i, bool pass) {
 #pragma clang fp contract(off)
   Axis a;
-  float g = 2.0f * loc - 1.0f;
-  a.pass = !clamp || (g >= lo && g <= hi);
-  if (clamp) g = fminf(fmaxf(g, lo), hi);
-  const float u = ((g + 1.0f) * size_f - 1.0f) * 0.5f;
   const float u0 = floorf(u);
   a.f = u - u0;
   a.e = (u0 + 1.0f) - u;
-  a.i0 = (int)fminf(fmaxf(u0, -2.0f), size_f + 1.0f);
+  a.i0 = (int)fminf(fmaxf(u0, -2.0f), (float)size_i + 1.0f);
   a.v0 = (unsigned)a.i0 < (unsigned)size_i;
   a.v1 = (unsigned)(a.i0 + 1) < (unsigned)size_i;
+  a.pass = pass;
   return a;
+}
+
+__device__ inline Axis make_axis(float loc, float size_f, int size_i, int clamp, float lo,
+                                 float hi) {
+  bool pass;
+  const float u = grid_to_u(loc, size_f, clamp, lo, hi, &pass);
+  return axis_from_u(u, size_i, pass);
 }
 
 // Level table entry: first row of the level in K, and its extents (D = 1 in 2D).
