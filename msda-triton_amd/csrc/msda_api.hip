@@ -37,8 +37,9 @@ const char* dtype_name(int dt) {
 }
 
 constexpr uint64_t kLim31 = 0x7FFFFFFFull;
-constexpr uint32_t kSubBatchesPerChunk = 16;  // records per chunk = 16 * S
-constexpr uint32_t kTileLdsBudget = 160 * 1024 - 256;
+constexpr uint32_t kChunkRecords = 4096;        // records per tile-kernel chunk (rounded to S)
+constexpr uint32_t kTileLdsTarget = 52 * 1024;  // three tile workgroups per CU (160 KB LDS)
+constexpr uint32_t kTileLdsBudget = 160 * 1024 - 256;  // one workgroup per CU
 constexpr int kMaxBinsLds = 8192;  // bin histogram + bases in 64 KB of LDS
 
 // Lanes per unit and per-lane vector width for one C-channel value row.
@@ -216,14 +217,16 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
                 "backward supports Q*P up to 2^27 per launch, got Q=%lld P=%d",
                 (long long)d->num_queries, d->num_points);
   // Tile extents and sub-batch size: start from 16x16 (2D) / 8x8x8 (3D) cells and 512
-  // records; shrink until a thread owns at most kTileMaxItems (region cell, chunk) items,
-  // the region has at most kTileThreads cells, and the staged value region, grad_out rows,
-  // records, sorted entries and counters fit in LDS.
-  int T[3] = {16, 16, 1};
-  if (d->dim == 3) T[0] = T[1] = T[2] = 8;
-  const uint32_t val_row = (uint32_t)(d->channels * s) + 16;  // +16 B spreads LDS banks
+  // records; halve S (down to 32) and then the largest tile extent until a thread owns at
+  // most kTileMaxItems (region cell, chunk) items, the region has at most 2 * kTileThreads
+  // cells, a thread stages at most kTileGradPerThread grad_out chunks and counts at most
+  // kTileRecPerThread records, and the staged grad_out rows, records, sorted entries and
+  // counters fit the LDS share of one of three workgroups per CU (or,
+  // for very wide heads, all of a CU's LDS).
+  const uint32_t NT = msda::kTileThreads;
   const uint32_t grow = (uint32_t)(d->channels * s);
-  uint32_t S = 512, lds = 0, vbytes = 0;
+  int T[3];
+  uint32_t S = 512, lds = 0;
   int rcells = 0;
   auto shrink = [&]() {
     const int k = (T[2] >= T[1] && T[2] >= T[0] && T[2] > 1) ? 2 : (T[1] >= T[0] && T[1] > 1 ? 1 : 0);
@@ -231,38 +234,60 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
     T[k] /= 2;
     return true;
   };
-  for (;;) {
-    const int rz = d->dim == 3 ? T[2] + 1 : 1;
-    rcells = (T[0] + 1) * (T[1] + 1) * rz;
-    vbytes = (((uint32_t)rcells * val_row) + 15) & ~15u;
-    lds = vbytes + S * grow + S * nc * 8u + S * rw * 4u +
-          (uint32_t)(2 * rcells + 1 + msda::kTileThreads / 64) * 4u;
-    if (rcells * lay.nvec > msda::kTileMaxItems * msda::kTileThreads || rcells > msda::kTileThreads) {
-      if (!shrink()) return fail(MSDA_ERR_INVALID, "channels per head too large for the backward");
-      continue;
+  // largest tile, then largest S, that meets the per-thread limits and the LDS budget
+  auto fit = [&](uint32_t budget) {
+    T[0] = T[1] = 16;
+    T[2] = 1;
+    if (d->dim == 3) T[0] = T[1] = T[2] = 8;
+    S = 512;
+    for (;;) {
+      const int rz = d->dim == 3 ? T[2] + 1 : 1;
+      rcells = (T[0] + 1) * (T[1] + 1) * rz;
+      lds = S * grow + S * nc * 8u + S * rw * 4u + (uint32_t)(rcells + 1 + NT / 64) * 4u;
+      if ((uint32_t)(rcells * lay.nvec) > msda::kTileMaxItems * NT || (uint32_t)rcells > 2 * NT) {
+        if (!shrink()) return false;
+        continue;
+      }
+      if (S <= msda::kTileRecPerThread * NT &&
+          S * (uint32_t)lay.nvec <= msda::kTileGradPerThread * NT && lds <= budget)
+        return true;
+      if (S > 32) {
+        S /= 2;
+        continue;
+      }
+      if (!shrink()) return false;
+      S = 512;
     }
-    if (lds <= kTileLdsBudget) break;
-    if (S > 128) {
-      S /= 2;
-      continue;
-    }
-    if (!shrink()) return fail(MSDA_ERR_INVALID, "channels per head too large for the backward");
-  }
+  };
+  if (!fit(kTileLdsTarget) && !fit(kTileLdsBudget))
+    return fail(MSDA_ERR_INVALID, "channels per head (%d) too large for the backward", d->channels);
   pl.TX = T[0];
   pl.TY = T[1];
   pl.TZ = T[2];
+  auto log2i = [](int v) {
+    int l = 0;
+    while ((1 << l) < v) ++l;
+    return l;
+  };
+  pl.tx_log2 = log2i(T[0]);
+  pl.ty_log2 = log2i(T[1]);
+  pl.tz_log2 = log2i(T[2]);
+  pl.div_nvec = msda::make_fastdiv((uint32_t)lay.nvec);
+  pl.div_rx = msda::make_fastdiv((uint32_t)(T[0] + 1));
+  pl.div_rxy = msda::make_fastdiv((uint32_t)((T[0] + 1) * (T[1] + 1)));
+  pl.div_tx = msda::make_fastdiv((uint32_t)T[0]);
+  pl.div_txy = msda::make_fastdiv((uint32_t)(T[0] * T[1]));
   pl.RX = T[0] + 1;
   pl.RY = T[1] + 1;
   pl.RZ = d->dim == 3 ? T[2] + 1 : 1;
   pl.cells = T[0] * T[1] * T[2];
   pl.rcells = rcells;
   pl.S = S;
-  pl.val_row_bytes = val_row;
-  pl.lds_val_bytes = vbytes;
   pl.lds_g_bytes = S * grow;
   pl.lds_bytes = lds;
+  // tiles of the coarsest level first: its chunks are the longest, so they start early
   int tiles = 0;
-  for (int l = 0; l < d->num_levels; ++l) {
+  for (int l = d->num_levels - 1; l >= 0; --l) {
     msda::BwdLevel& lv = pl.lv[l];
     lv.ntx = (lv.W + pl.TX - 1) / pl.TX;
     lv.nty = (lv.H + pl.TY - 1) / pl.TY;
@@ -273,6 +298,7 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
       return fail(MSDA_ERR_INVALID,
                   "backward: levels too large (%lld tiles per head; the binning supports %d)",
                   (long long)(tiles + nt), kMaxBinsLds);
+    lv.ntiles = (int32_t)nt;
     tiles += (int)nt;
   }
   int hg = lay.hg_log2;
@@ -284,11 +310,14 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
   pl.K = (int32_t)d->num_keys;
   pl.Q = (uint32_t)d->num_queries;
   pl.div_p = msda::make_fastdiv((uint32_t)(d->num_points > 0 ? d->num_points : 1));
+  pl.div_lp = msda::make_fastdiv((uint32_t)(d->num_levels * d->num_points > 0
+                                                ? d->num_levels * d->num_points : 1));
   pl.tiles_per_bh = tiles;
   pl.hg_log2 = hg;
   pl.bins = tiles << hg;
-  pl.wgpg = (int32_t)(((uint64_t)d->num_queries << hg) + msda::kBlock - 1) / msda::kBlock;
-  pl.R = kSubBatchesPerChunk * pl.S;
+  pl.upw = (msda::kGradThreads >> lay.lpu_log2) * msda::kGradRounds;
+  pl.wgpg = (int32_t)((((uint64_t)d->num_queries << hg) + pl.upw - 1) / pl.upw);
+  pl.R = (kChunkRecords + pl.S - 1) / pl.S * pl.S;
   pl.lpu_log2 = lay.lpu_log2;
   pl.nvec = lay.nvec;
   pl.clamp = d->clamp_grid ? 1 : 0;
@@ -445,6 +474,8 @@ int msda_bwd(const msda_desc* d, const int32_t* host_spatial_shapes, const void*
     bf.grad_value = static_cast<char*>(grad_value) + (uint64_t)b0 * kv * sv;
     bf.grad_loc = static_cast<char*>(grad_sampling_locations) + (uint64_t)b0 * qh * LP * d->dim * sc;
     bf.grad_attn = static_cast<char*>(grad_attention_weights) + (uint64_t)b0 * qh * LP * sc;
+    pl.coords_aligned = aligned(bf.loc, 16) && aligned(bf.attn, 16) && aligned(bf.grad_loc, 16) &&
+                        aligned(bf.grad_attn, 16);
     hipError_t e = msda::run_bwd(pl, bf, d->dim, d->value_dtype, d->coord_dtype,
                                  hp.lay.vec_bytes, st);
     if (e != hipSuccess) return fail(MSDA_ERR_HIP, "msda_bwd launch failed: %s", hipGetErrorString(e));

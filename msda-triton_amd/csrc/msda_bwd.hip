@@ -7,26 +7,30 @@
 // random rows sustain about 0.33 T element-adds/s and LDS fp32 atomics about a third of
 // an operation per clock per CU, so this backward accumulates grad_value in key order:
 //
-//  1. bin count: every sample with a valid corner is assigned to the tile of its level
-//     that owns its lowest corner. Each workgroup covers the units of one (batch,
-//     head-group), histograms its samples per tile in LDS (integer atomics, full rate),
-//     and writes the histogram as one row of a per-(workgroup, tile) count matrix.
-//  2. column scan: per tile, the counts of all workgroups become offsets within the tile
-//     and the tile's total.
+//  1. sample gradients + count: one lane group per unit (b, q, h), as in the forward:
+//     the unit's grad_out row is read once into registers, each sample's corner rows are
+//     gathered from L2 (value slices stay XCD-resident) and grad_attention_weights and
+//     grad_sampling_locations are stored per unit. Every sample with a valid corner is
+//     also assigned to the tile of its level that owns its lowest corner; each workgroup
+//     (upw units of one (batch, head-group)) histograms its samples per tile in LDS
+//     (integer atomics, full rate) and writes the histogram as one column of a tile-major
+//     (tile, workgroup) count matrix.
+//  2. column scan (one wave per tile): the tile's counts over the workgroups become
+//     offsets within the tile, and the tile's total.
 //  3. plan (one workgroup): exclusive scan of the tile totals, chunks of at most R records
 //     per tile, and the chunk -> tile table.
-//  4. bin fill: the same traversal writes each sample's record (id, clamp flags, pixel
-//     coordinates, attention weight) at its tile's base + offset + LDS rank, so later
-//     passes never re-read locations or weights at random addresses.
+//  4. fill: per level, each workgroup ranks its samples per tile in LDS, sorts their
+//     records (id, clamp flags, pixel coordinates, attention weight) by tile in LDS and
+//     writes them out as contiguous runs.
 //  5. tile kernel: one workgroup per chunk, chunks of one (batch, head-group) on one XCD.
-//     It stages the tile's value region (tile + one-cell high-side halo) in LDS; per
-//     sub-batch of S records it stages grad_out rows, forms <grad_out, value_corner> from
-//     the staged rows and stores grad_attention_weights and grad_sampling_locations,
-//     sorts the (corner weight * attn, record) entries by region cell, and accumulates
-//     grad_value for every region cell in the fp32 registers of the cell's owner threads.
-//     Interior cells of a one-chunk tile are written directly in the value dtype; edge
-//     cells (which also receive halo contributions of lower neighbours), halo cells and
-//     every cell of a split tile are written as fp32 partials.
+//     Per sub-batch of S records it stages the records and their grad_out rows (two
+//     coalesced round trips), sorts the (corner weight * attn, record) entries by cell of
+//     the tile's region (the tile plus a one-cell high-side halo, which holds every corner
+//     of a sample anchored in the tile; ranks come from the counting atomics), and
+//     accumulates grad_value for every region cell in the fp32 registers of the cell's
+//     owner threads. Interior cells of a one-chunk tile are written directly in the value
+//     dtype; edge cells (which also receive halo contributions of lower neighbours), halo
+//     cells and every cell of a split tile are written as fp32 partials.
 //  6. fold: per tile, sums the partials of its own chunks and the halo partials of its
 //     lower neighbours' chunks, in a fixed order, and writes the edge / split cells.
 //
@@ -78,19 +82,23 @@ struct TileCoord {
   int l, tx, ty, tz, X0, Y0, Z0;
 };
 
+__device__ inline int level_of_tile(const BwdPlan& pl, int tib) {
+  int l = 0;
+  while (l + 1 < pl.L && !(tib >= pl.lv[l].tile_off && tib < pl.lv[l].tile_off + pl.lv[l].ntiles)) ++l;
+  return l;
+}
+
 __device__ inline TileCoord decode_tile(const BwdPlan& pl, uint32_t t) {
   TileCoord tc;
   tc.g = t / (uint32_t)pl.bins;
   const uint32_t bin = t - tc.g * (uint32_t)pl.bins;
-  tc.hsub = bin / (uint32_t)pl.tiles_per_bh;
-  const int tib = (int)(bin - tc.hsub * (uint32_t)pl.tiles_per_bh);
+  tc.hsub = bin & ((1u << pl.hg_log2) - 1u);
+  const int tib = (int)(bin >> pl.hg_log2);
   const uint32_t gph = (uint32_t)pl.H >> pl.hg_log2;
   tc.b = tc.g / gph;
   tc.h = ((tc.g - tc.b * gph) << pl.hg_log2) | tc.hsub;
-  int l = 0;
-  while (l + 1 < pl.L && pl.lv[l + 1].tile_off <= tib) ++l;
-  tc.l = l;
-  const BwdLevel& lv = pl.lv[l];
+  tc.l = level_of_tile(pl, tib);
+  const BwdLevel& lv = pl.lv[tc.l];
   const int lt = tib - lv.tile_off;
   tc.tx = lt % lv.ntx;
   tc.ty = (lt / lv.ntx) % lv.nty;
@@ -109,102 +117,269 @@ __device__ inline int region_cell(const BwdPlan& pl, int ox, int oy, int oz) {
   return (oz * pl.RY + oy) * pl.RX + ox;
 }
 
-// ------------------------------------------------------------------ 1, 4: binning
-// One thread per unit (b, q, h) of a (batch, head-group): u = w * kBlock + tid enumerates
-// (q, head-in-group). FILL = false counts samples per tile; FILL = true writes records.
-template <int DIM, typename EC, bool FILL>
-__global__ __launch_bounds__(kBlock) void bwd_bin_kernel(const BwdPlan pl, const BwdBuffers bf) {
-  typedef typename EC::T TC;
-  extern __shared__ uint32_t s_hist[];  // [bins] counters, then [bins] record bases (fill)
-  uint32_t* s_base = s_hist + pl.bins;
-  const uint32_t g = blockIdx.x / (uint32_t)pl.wgpg;
-  const uint32_t w = blockIdx.x - g * (uint32_t)pl.wgpg;
-  const size_t crow = ((size_t)g * pl.wgpg + w) * pl.bins;
-  for (int i = threadIdx.x; i < pl.bins; i += kBlock) {
-    s_hist[i] = 0;
-    if (FILL) s_base[i] = bf.bin_start[(size_t)g * pl.bins + i] + bf.counts[crow + i];
+// Unit of a bin workgroup: the wi-th of the upw units of workgroup w of group g.
+struct BinUnit {
+  uint32_t q, hsub, b, h;
+  size_t bqh;
+};
+
+__device__ inline BinUnit bin_unit(const BwdPlan& pl, uint32_t g, uint32_t w, uint32_t wi) {
+  BinUnit bu;
+  const uint32_t U = w * (uint32_t)pl.upw + wi;
+  bu.q = U >> pl.hg_log2;
+  bu.hsub = U & ((1u << pl.hg_log2) - 1u);
+  const uint32_t gph = (uint32_t)pl.H >> pl.hg_log2;
+  bu.b = g / gph;
+  bu.h = ((g - bu.b * gph) << pl.hg_log2) | bu.hsub;
+  bu.bqh = ((size_t)bu.b * pl.Q + bu.q) * pl.H + bu.h;
+  return bu;
+}
+
+// Pixel coordinates, clamp flags and anchor tile of one sample; false if the sample has
+// no corner inside its level.
+template <int DIM, typename TC>
+__device__ inline bool sample_tile(const BwdPlan& pl, const BwdLevel& lv, const TC* lp, float* u,
+                                   uint32_t* flags, int* tib) {
+  bool px, py, pz = true;
+  u[0] = grid_to_u((float)lp[0], (float)lv.W, pl.clamp, pl.lo_g, pl.hi_g, &px);
+  u[1] = grid_to_u((float)lp[1], (float)lv.H, pl.clamp, pl.lo_g, pl.hi_g, &py);
+  u[2] = 0.0f;
+  if constexpr (DIM == 3) u[2] = grid_to_u((float)lp[2], (float)lv.D, pl.clamp, pl.lo_g, pl.hi_g, &pz);
+  const Axis ax = axis_from_u(u[0], lv.W, px);
+  const Axis ay = axis_from_u(u[1], lv.H, py);
+  const Axis az = DIM == 3 ? axis_from_u(u[2], lv.D, pz) : Axis{1.0f, 0.0f, 0, true, false, true};
+  if (!(ax.v0 || ax.v1) || !(ay.v0 || ay.v1) || !(az.v0 || az.v1)) return false;
+  const int tx = anchor_tile(ax, pl.tx_log2), ty = anchor_tile(ay, pl.ty_log2);
+  const int tz = DIM == 3 ? anchor_tile(az, pl.tz_log2) : 0;
+  *tib = lv.tile_off + (tz * lv.nty + ty) * lv.ntx + tx;
+  *flags = (px ? kRecPassX : 0u) | (py ? kRecPassY : 0u) | (pz ? kRecPassZ : 0u);
+  return true;
+}
+
+// ------------------------------------------------------------------ 1: sample gradients
+// Gradients of one sample from its gathered corner rows: <grad_out, v_c> per corner, then
+// d/d(attn) and (clamp-masked) d/d(loc) summed over the unit's lanes, so every lane of
+// the group holds them. out = {grad_attn, grad_loc x, y[, z]}.
+template <int DIM, typename EV, int VEC, int NC = (1 << DIM)>
+__device__ inline void sample_grads(const BwdPlan& pl, const BwdLevel& lv, const Sample<DIM>& sm,
+                                    const RawVec<VEC * EV::kBytes> (&raw)[NC], const float (&gr)[VEC],
+                                    float a, float (&out)[DIM + 1]) {
+  float dot[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    float v[VEC];
+    widen<EV, VEC>(raw[c], v);
+    float d = 0.0f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) d = __builtin_fmaf(gr[e], v[e], d);
+    dot[c] = d;
   }
+  float s_attn, s_x, s_y, s_z;
+  corner_grads<DIM>(sm, dot, s_attn, s_x, s_y, s_z);
+  const int lg = pl.lpu_log2;
+  out[0] = group_sum(s_attn, lg);
+  s_x = group_sum(s_x, lg);
+  s_y = group_sum(s_y, lg);
+  out[1] = sm.ax.pass ? (a * s_x) * (float)lv.W : 0.0f;
+  out[2] = sm.ay.pass ? (a * s_y) * (float)lv.H : 0.0f;
+  if constexpr (DIM == 3) {
+    s_z = group_sum(s_z, lg);
+    out[3] = sm.az.pass ? (a * s_z) * (float)lv.D : 0.0f;
+  }
+}
+
+// Axes, corner-row offsets and anchor bin of one sample from its DIM coordinates.
+template <int DIM>
+__device__ inline bool sample_rows(const BwdPlan& pl, const BwdLevel& lv, const float* xyz,
+                                   uint32_t vbase, uint32_t rs, uint32_t hsub, Sample<DIM>& sm,
+                                   uint32_t (&off)[1 << DIM], uint32_t* bin) {
+  bool px, py, pz = true;
+  const float ux = grid_to_u(xyz[0], (float)lv.W, pl.clamp, pl.lo_g, pl.hi_g, &px);
+  const float uy = grid_to_u(xyz[1], (float)lv.H, pl.clamp, pl.lo_g, pl.hi_g, &py);
+  sm.ax = axis_from_u(ux, lv.W, px);
+  sm.ay = axis_from_u(uy, lv.H, py);
+  const uint32_t W = (uint32_t)lv.W, HW = (uint32_t)lv.W * (uint32_t)lv.H;
+  uint32_t row0 = (uint32_t)lv.start + (uint32_t)sm.ay.i0 * W + (uint32_t)sm.ax.i0;
+  bool any = (sm.ax.v0 || sm.ax.v1) && (sm.ay.v0 || sm.ay.v1);
+  int tz = 0;
+  if constexpr (DIM == 3) {
+    const float uz = grid_to_u(xyz[2], (float)lv.D, pl.clamp, pl.lo_g, pl.hi_g, &pz);
+    sm.az = axis_from_u(uz, lv.D, pz);
+    row0 += (uint32_t)sm.az.i0 * HW;
+    any = any && (sm.az.v0 || sm.az.v1);
+    tz = any ? anchor_tile(sm.az, pl.tz_log2) : 0;
+  }
+  const uint32_t off0 = vbase + row0 * rs;
+#pragma unroll
+  for (int c = 0; c < (1 << DIM); ++c) {
+    const uint32_t dr = ((c & 1) ? 1u : 0u) + ((c & 2) ? W : 0u) + ((DIM == 3 && (c & 4)) ? HW : 0u);
+    off[c] = corner_valid<DIM>(c, sm) ? off0 + dr * rs : kOobOffset;
+  }
+  if (any) {
+    const int tib = lv.tile_off + (tz * lv.nty + anchor_tile(sm.ay, pl.ty_log2)) * lv.ntx +
+                    anchor_tile(sm.ax, pl.tx_log2);
+    *bin = ((uint32_t)tib << pl.hg_log2) | hsub;
+  }
+  return any;
+}
+
+// One lane group of 2^lpu_log2 lanes per unit (b, q, h), with the forward's work layout:
+// lane j holds channels [j*VEC, (j+1)*VEC) of the unit's grad_out row; corners outside
+// the level read as zero through the buffer range check, so samples without a valid
+// corner get zero gradients. PT > 0: P is a compile-time constant; each batch's
+// coordinates and weights are one block load per lane, queued behind the previous
+// batch's corner rows, and all SB*2^DIM corner rows of a batch are in flight together.
+template <int DIM, typename EV, typename EC, int VEC, int PT>
+__global__ __launch_bounds__(kGradThreads) void bwd_grad_kernel(const BwdPlan pl, const BwdBuffers bf) {
+  constexpr int VB = VEC * EV::kBytes;
+  constexpr int NC = 1 << DIM;
+  constexpr int SB = PT > 0 ? (DIM == 2 ? (PT < 4 ? PT : 4) : (PT < 2 ? PT : 2)) : (DIM == 2 ? 2 : 1);
+  typedef typename EC::T TC;
+  typedef typename EV::T TV;
+  extern __shared__ uint32_t s_hist[];  // [bins]
+  // workgroups of one (batch, head-group) are contiguous and dealt to one XCD
+  const uint32_t lb = xcd_logical_block(blockIdx.x, gridDim.x);
+  const uint32_t g = lb / (uint32_t)pl.wgpg;
+  const uint32_t w = lb - g * (uint32_t)pl.wgpg;
+  for (int i = threadIdx.x; i < pl.bins; i += kGradThreads) s_hist[i] = 0;
   __syncthreads();
 
-  const uint32_t HG = 1u << pl.hg_log2;
-  const uint32_t u = w * kBlock + threadIdx.x;
-  if (u < pl.Q * HG) {
-    const uint32_t q = u >> pl.hg_log2, hsub = u & (HG - 1u);
-    const uint32_t gph = (uint32_t)pl.H >> pl.hg_log2;
-    const uint32_t b = g / gph, h = ((g - b * gph) << pl.hg_log2) | hsub;
-    const int LP = pl.L * pl.P;
-    const size_t bqh = ((size_t)b * pl.Q + q) * pl.H + h;
-    const TC* locp = static_cast<const TC*>(bf.loc) + bqh * LP * DIM;
-    const TC* attp = static_cast<const TC*>(bf.attn) + bqh * LP;
-    for (int l = 0; l < pl.L; ++l) {
-      const BwdLevel& lv = pl.lv[l];
-      for (int p = 0; p < pl.P; ++p) {
-        const int s = l * pl.P + p;
-        bool px, py, pz = true;
-        const float ux = grid_to_u((float)locp[s * DIM + 0], (float)lv.W, pl.clamp, pl.lo_g, pl.hi_g, &px);
-        const float uy = grid_to_u((float)locp[s * DIM + 1], (float)lv.H, pl.clamp, pl.lo_g, pl.hi_g, &py);
-        float uz = 0.0f;
-        if constexpr (DIM == 3)
-          uz = grid_to_u((float)locp[s * DIM + 2], (float)lv.D, pl.clamp, pl.lo_g, pl.hi_g, &pz);
-        const Axis ax = axis_from_u(ux, lv.W, px);
-        const Axis ay = axis_from_u(uy, lv.H, py);
-        const Axis az = DIM == 3 ? axis_from_u(uz, lv.D, pz) : Axis{1.0f, 0.0f, 0, true, false, true};
-        if (!(ax.v0 || ax.v1) || !(ay.v0 || ay.v1) || !(az.v0 || az.v1)) {
-          // no corner inside the level: the sample's gradients are zero
-          if (!FILL) {
-            TC* gl = static_cast<TC*>(bf.grad_loc) + (bqh * LP + s) * DIM;
+  const int lg = pl.lpu_log2;
+  const uint32_t lanes = 1u << lg;
+  const uint32_t lane = threadIdx.x & (lanes - 1u);
+  const bool act = (int)lane < pl.nvec;
+  const uint32_t gpw = (uint32_t)kGradThreads >> lg;  // unit groups per workgroup
+  const uint32_t units = min((uint32_t)pl.upw, (pl.Q << pl.hg_log2) - w * (uint32_t)pl.upw);
+  const int LP = pl.L * pl.P;
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(bf.value, pl.value_bytes);
+  const uint32_t rs = (uint32_t)pl.H * (uint32_t)pl.C * EV::kBytes;  // bytes between rows of K
+#pragma unroll 1
+  for (uint32_t wi = threadIdx.x >> lg; wi < units; wi += gpw) {
+    const BinUnit bu = bin_unit(pl, g, w, wi);
+    float gr[VEC];
+    if (act) {
+      widen<EV, VEC>(glb_load<VB>(static_cast<const TV*>(bf.grad_out) + bu.bqh * pl.C + lane * VEC), gr);
+    } else {
 #pragma unroll
-            for (int d = 0; d < DIM; ++d) gl[d] = (TC)0.0f;
-            static_cast<TC*>(bf.grad_attn)[bqh * LP + s] = (TC)0.0f;
-          }
-          continue;
+      for (int k = 0; k < VEC; ++k) gr[k] = 0.0f;
+    }
+    const uint32_t vbase =
+        ((bu.b * (uint32_t)pl.K * (uint32_t)pl.H + bu.h) * (uint32_t)pl.C + (act ? lane : 0u) * VEC) *
+        EV::kBytes;
+    const TC* locp = static_cast<const TC*>(bf.loc) + bu.bqh * LP * DIM;
+    const TC* attp = static_cast<const TC*>(bf.attn) + bu.bqh * LP;
+    TC* glp = static_cast<TC*>(bf.grad_loc) + bu.bqh * LP * DIM;
+    TC* gap = static_cast<TC*>(bf.grad_attn) + bu.bqh * LP;
+    if constexpr (PT > 0) {
+      constexpr int BPL = PT / SB;  // batches per level
+      CoordBlock<EC, SB * DIM> cb;
+      CoordBlock<EC, SB> ab;
+      const int nbatch = pl.L * BPL;
+      if (nbatch > 0) {
+        load_block<EC, SB * DIM>(cb, locp);
+        load_block<EC, SB>(ab, attp);
+      }
+#pragma unroll 1
+      for (int bi = 0; bi < nbatch; ++bi) {
+        const BwdLevel& lv = pl.lv[bi / BPL];
+        Sample<DIM> sm[SB];
+        uint32_t off[SB][NC], bin[SB];
+        bool any[SB];
+        float a[SB];
+#pragma unroll
+        for (int k = 0; k < SB; ++k) {
+          float xyz[3];
+#pragma unroll
+          for (int d = 0; d < DIM; ++d) xyz[d] = block_elem(cb, k * DIM + d);
+          bin[k] = 0;
+          any[k] = sample_rows<DIM>(pl, lv, xyz, vbase, rs, bu.hsub, sm[k], off[k], &bin[k]);
+          a[k] = block_elem(ab, k);
         }
-        const int tx = anchor_tile(ax, pl.TX), ty = anchor_tile(ay, pl.TY);
-        const int tz = DIM == 3 ? anchor_tile(az, pl.TZ) : 0;
-        const int tib = lv.tile_off + (tz * lv.nty + ty) * lv.ntx + tx;
-        const uint32_t bin = hsub * (uint32_t)pl.tiles_per_bh + (uint32_t)tib;
-        const uint32_t r = atomicAdd(&s_hist[bin], 1u);
-        if (FILL) {
-          const uint32_t id = (q * (uint32_t)pl.P + (uint32_t)p) | (px ? kRecPassX : 0u) |
-                              (py ? kRecPassY : 0u) | (pz ? kRecPassZ : 0u);
-          const float a = (float)attp[s];
-          uint32_t* rec = bf.records + (size_t)(s_base[bin] + r) * (DIM + 2);
-          if constexpr (DIM == 2) {
-            *reinterpret_cast<u32x4*>(rec) =
-                u32x4{id, __builtin_bit_cast(uint32_t, ux), __builtin_bit_cast(uint32_t, uy),
-                      __builtin_bit_cast(uint32_t, a)};
-          } else {
-            rec[0] = id;
-            rec[1] = __builtin_bit_cast(uint32_t, ux);
-            rec[2] = __builtin_bit_cast(uint32_t, uy);
-            rec[3] = __builtin_bit_cast(uint32_t, uz);
-            rec[4] = __builtin_bit_cast(uint32_t, a);
+        RawVec<VB> raw[SB][NC];
+#pragma unroll
+        for (int k = 0; k < SB; ++k)
+#pragma unroll
+          for (int c = 0; c < NC; ++c) raw[k][c] = buf_load<VB>(rv, off[k][c]);
+        if (bi + 1 < nbatch) {
+          load_block<EC, SB * DIM>(cb, locp + (bi + 1) * (SB * DIM));
+          load_block<EC, SB>(ab, attp + (bi + 1) * SB);
+        }
+        float ga[SB], gl[SB * DIM];
+#pragma unroll
+        for (int k = 0; k < SB; ++k) {
+          float o[DIM + 1];
+          sample_grads<DIM, EV, VEC>(pl, lv, sm[k], raw[k], gr, a[k], o);
+          ga[k] = o[0];
+#pragma unroll
+          for (int d = 0; d < DIM; ++d) gl[k * DIM + d] = o[1 + d];
+          if (any[k] && lane == ((uint32_t)k & (lanes - 1u))) atomicAdd(&s_hist[bin[k]], 1u);
+        }
+        // the batch's gradients are contiguous per unit: one block store each
+        if (lane == 0) {
+          store_block<EC, SB>(gap + bi * SB, ga);
+          store_block<EC, SB * DIM>(glp + bi * (SB * DIM), gl);
+        }
+      }
+    } else {
+      for (int l = 0; l < pl.L; ++l) {
+        const BwdLevel& lv = pl.lv[l];
+#pragma unroll 1
+        for (int p0 = 0; p0 < pl.P; p0 += SB) {
+          Sample<DIM> sm[SB];
+          uint32_t off[SB][NC], bin[SB];
+          bool any[SB];
+          RawVec<VB> raw[SB][NC];
+#pragma unroll
+          for (int k = 0; k < SB; ++k) {
+            const bool live = p0 + k < pl.P;
+            const int s = l * pl.P + (live ? p0 + k : 0);
+            float xyz[3];
+#pragma unroll
+            for (int d = 0; d < DIM; ++d) xyz[d] = (float)locp[s * DIM + d];
+            bin[k] = 0;
+            any[k] = sample_rows<DIM>(pl, lv, xyz, vbase, rs, bu.hsub, sm[k], off[k], &bin[k]);
+#pragma unroll
+            for (int c = 0; c < NC; ++c) raw[k][c] = buf_load<VB>(rv, live ? off[k][c] : kOobOffset);
+          }
+#pragma unroll
+          for (int k = 0; k < SB; ++k) {
+            if (p0 + k >= pl.P) continue;
+            const int s = l * pl.P + p0 + k;
+            float o[DIM + 1];
+            sample_grads<DIM, EV, VEC>(pl, lv, sm[k], raw[k], gr, (float)attp[s], o);
+            if (lane == ((uint32_t)k & (lanes - 1u))) {
+              gap[s] = (TC)o[0];
+#pragma unroll
+              for (int d = 0; d < DIM; ++d) glp[s * DIM + d] = (TC)o[1 + d];
+              if (any[k]) atomicAdd(&s_hist[bin[k]], 1u);
+            }
           }
         }
       }
     }
   }
-  if (!FILL) {
-    __syncthreads();
-    for (int i = threadIdx.x; i < pl.bins; i += kBlock) bf.counts[crow + i] = s_hist[i];
-  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < pl.bins; i += kGradThreads)
+    bf.counts[((size_t)g * pl.bins + i) * pl.wgpg + w] = s_hist[i];
 }
 
 // ------------------------------------------------------------------ 2: column scan
-// One thread per tile: the tile's counts over the bin workgroups of its group become
+// One wave per tile: the tile's counts over the bin workgroups of its group become
 // offsets within the tile, and its total goes to bin_start[t].
 __global__ __launch_bounds__(kBlock) void bwd_colscan_kernel(const BwdPlan pl, const BwdBuffers bf) {
-  const uint32_t t = blockIdx.x * kBlock + threadIdx.x;
-  if (t >= pl.T) return;
-  const uint32_t g = t / (uint32_t)pl.bins, i = t - g * (uint32_t)pl.bins;
+  const uint32_t t = blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
+  const uint32_t lane = threadIdx.x & (kWave - 1);
+  if (t >= pl.T) return;  // the whole wave exits
+  uint32_t* c = bf.counts + (size_t)t * pl.wgpg;
   uint32_t run = 0;
-  for (int w = 0; w < pl.wgpg; ++w) {
-    const size_t idx = ((size_t)g * pl.wgpg + w) * pl.bins + i;
-    const uint32_t c = bf.counts[idx];
-    bf.counts[idx] = run;
-    run += c;
+  for (int base = 0; base < pl.wgpg; base += kWave) {
+    const int i = base + (int)lane;
+    const uint32_t v = i < pl.wgpg ? c[i] : 0u;
+    const uint32_t inc = wave_incl_scan(v);
+    if (i < pl.wgpg) c[i] = run + inc - v;
+    run += __shfl(inc, kWave - 1, kWave);
   }
-  bf.bin_start[t] = run;
+  if (lane == 0) bf.bin_start[t] = run;
 }
 
 // ------------------------------------------------------------------ 3: plan
@@ -239,6 +414,104 @@ __global__ __launch_bounds__(kPlanThreads) void bwd_plan_kernel(const BwdPlan pl
   }
 }
 
+// ------------------------------------------------------------------ 4: fill
+// Same workgroup -> units mapping as the sample-gradient kernel. Per level, in rounds of at most
+// kFillStage samples: rank each sample within its bin (LDS atomics), scan the round's
+// per-bin counts, place the records in LDS sorted by bin, and copy them out so that
+// consecutive threads write consecutive records of one bin.
+template <int DIM, typename EC>
+__global__ __launch_bounds__(kBlock) void bwd_fill_kernel(const BwdPlan pl, const BwdBuffers bf) {
+  typedef typename EC::T TC;
+  constexpr int RW = DIM + 2;
+  constexpr int KP = kFillStage / kBlock;  // samples per thread per round
+  extern __shared__ uint32_t s_fill[];
+  uint32_t* s_base = s_fill;               // [bins] next global record of each bin
+  uint32_t* s_cnt = s_base + pl.bins;      // [bins] round counts -> round offsets
+  uint32_t* s_rec = s_cnt + pl.bins;       // [kFillStage * RW] records sorted by bin
+  uint32_t* s_key = s_rec + kFillStage * RW;  // [kFillStage] bin of each sorted record
+  uint32_t* s_w = s_key + kFillStage;      // [kBlock / kWave]
+  const uint32_t g = blockIdx.x / (uint32_t)pl.wgpg;
+  const uint32_t w = blockIdx.x - g * (uint32_t)pl.wgpg;
+  for (int i = threadIdx.x; i < pl.bins; i += kBlock)
+    s_base[i] = bf.bin_start[(size_t)g * pl.bins + i] + bf.counts[((size_t)g * pl.bins + i) * pl.wgpg + w];
+  const uint32_t units = min((uint32_t)pl.upw, (pl.Q << pl.hg_log2) - w * (uint32_t)pl.upw);
+  const int LP = pl.L * pl.P;
+  for (int l = 0; l < pl.L; ++l) {
+    const BwdLevel& lv = pl.lv[l];
+    const uint32_t lb0 = (uint32_t)lv.tile_off << pl.hg_log2;
+    const uint32_t lb1 = (uint32_t)(lv.tile_off + lv.ntiles) << pl.hg_log2;
+    const uint32_t n = units * (uint32_t)pl.P;
+    for (uint32_t r0 = 0; r0 < n; r0 += kFillStage) {
+      const uint32_t nr = min((uint32_t)kFillStage, n - r0);
+      for (uint32_t i = lb0 + threadIdx.x; i < lb1; i += kBlock) s_cnt[i] = 0;
+      __syncthreads();
+      // rank each sample of the round within its bin
+      uint32_t key[KP];
+#pragma unroll
+      for (int k = 0; k < KP; ++k) {
+        key[k] = 0xffffffffu;
+        const uint32_t j = threadIdx.x + k * kBlock;
+        if (j >= nr) continue;
+        const uint32_t js = r0 + j;
+        const uint32_t wi = fdiv(js, pl.div_p), p = js - wi * (uint32_t)pl.P;
+        const BinUnit bu = bin_unit(pl, g, w, wi);
+        const size_t si = bu.bqh * LP + (size_t)l * pl.P + p;
+        float u[3];
+        uint32_t flags;
+        int tib;
+        if (!sample_tile<DIM>(pl, lv, static_cast<const TC*>(bf.loc) + si * DIM, u, &flags, &tib)) continue;
+        const uint32_t bin = ((uint32_t)tib << pl.hg_log2) | bu.hsub;
+        key[k] = (bin << 16) | atomicAdd(&s_cnt[bin], 1u);
+      }
+      __syncthreads();
+      // exclusive scan of the round's counts over the level's bins
+      uint32_t carry = 0;
+      for (uint32_t b0 = lb0; b0 < lb1; b0 += kBlock) {
+        const uint32_t i = b0 + threadIdx.x;
+        const uint32_t v = i < lb1 ? s_cnt[i] : 0u;
+        uint32_t tot;
+        const uint32_t ex = block_excl_scan<kBlock>(v, s_w, &tot);
+        if (i < lb1) s_cnt[i] = carry + ex;
+        carry += tot;
+      }
+      __syncthreads();
+      // place the records sorted by bin
+#pragma unroll
+      for (int k = 0; k < KP; ++k) {
+        if (key[k] == 0xffffffffu) continue;
+        const uint32_t bin = key[k] >> 16, pos = s_cnt[bin] + (key[k] & 0xffffu);
+        const uint32_t js = r0 + threadIdx.x + k * kBlock;
+        const uint32_t wi = fdiv(js, pl.div_p), p = js - wi * (uint32_t)pl.P;
+        const BinUnit bu = bin_unit(pl, g, w, wi);
+        const size_t si = bu.bqh * LP + (size_t)l * pl.P + p;
+        float u[3];
+        uint32_t flags;
+        int tib;
+        sample_tile<DIM>(pl, lv, static_cast<const TC*>(bf.loc) + si * DIM, u, &flags, &tib);
+        uint32_t* rec = s_rec + pos * RW;
+        rec[0] = (bu.q * (uint32_t)pl.P + p) | flags;
+        rec[1] = __builtin_bit_cast(uint32_t, u[0]);
+        rec[2] = __builtin_bit_cast(uint32_t, u[1]);
+        if constexpr (DIM == 3) rec[3] = __builtin_bit_cast(uint32_t, u[2]);
+        rec[RW - 1] = __builtin_bit_cast(uint32_t, (float)static_cast<const TC*>(bf.attn)[si]);
+        s_key[pos] = bin;
+      }
+      __syncthreads();
+      // copy out: consecutive threads write consecutive records of a bin
+      for (uint32_t i = threadIdx.x; i < carry * RW; i += kBlock) {
+        const uint32_t r = i / RW, k = i - r * RW;
+        const uint32_t bin = s_key[r];
+        bf.records[(size_t)(s_base[bin] + (r - s_cnt[bin])) * RW + k] = s_rec[i];
+      }
+      __syncthreads();
+      // advance the bins' global positions by the round's counts
+      for (uint32_t i = lb0 + threadIdx.x; i < lb1; i += kBlock)
+        s_base[i] += (i + 1 < lb1 ? s_cnt[i + 1] : carry) - s_cnt[i];
+      __syncthreads();  // the next round clears s_cnt
+    }
+  }
+}
+
 // Axes of a staged record.
 template <int DIM>
 __device__ inline Sample<DIM> record_sample(const uint32_t* rec, const BwdLevel& lv) {
@@ -250,26 +523,33 @@ __device__ inline Sample<DIM> record_sample(const uint32_t* rec, const BwdLevel&
   return sm;
 }
 
+template <int DIM>
+__device__ inline int corner_cell(const BwdPlan& pl, const TileCoord& tc, const Sample<DIM>& sm, int cc) {
+  return region_cell(pl, sm.ax.i0 + (cc & 1) - tc.X0, sm.ay.i0 + ((cc >> 1) & 1) - tc.Y0,
+                     DIM == 3 ? sm.az.i0 + ((cc >> 2) & 1) - tc.Z0 : 0);
+}
+
 // ------------------------------------------------------------------ 5: tile kernel
-// One workgroup (kTileThreads threads) per chunk of a tile's records. LDS holds the staged
-// value region, and per sub-batch of up to S records: each record's grad_out row, the
-// record itself, the (weight, record) entries of its corners sorted by region cell, and
-// per-cell counters. Per sub-batch:
-//   A. record pass (2^lpu_log2 lanes per record): stage the record and its grad_out row;
-//      form <grad_out, value_corner> from the staged value rows and store
-//      grad_attention_weights / grad_sampling_locations; count corners per region cell.
-//   B. exclusive scan of the per-cell counts.
-//   C. entry pass (one thread per record): place (attn * w_corner, record) entries of the
-//      record's corners at their cell's offset + rank.
-//   D. owner pass: the thread owning (region cell, channel chunk) sums attn*w*grad_out over
-//      its cell's entries in fp32 registers.
+// One workgroup (kTileThreads threads) per chunk of a tile's records. LDS holds, per
+// sub-batch of up to S records: the records, their grad_out rows, the (weight, record)
+// entries of their corners sorted by region cell, and per-cell counts. Per sub-batch:
+//   A1. copy the records (coalesced) and clear the counters;
+//   A2. stage the grad_out rows (all loads of a thread issued before any is stored) and
+//       count corners per region cell, keeping each corner's rank;
+//   B.  exclusive scan of the per-cell counts;
+//   C.  place the entries at offset + rank;
+//   D.  the thread owning (region cell, channel chunk) sums attn*w*grad_out over its
+//       cell's entries in fp32 registers.
 template <int DIM, typename EV, typename EC, int VEC>
-__global__ __launch_bounds__(kTileThreads) void bwd_tile_kernel(const BwdPlan pl,
+__global__ __launch_bounds__(kTileThreads, kTileWavesPerSimd) void bwd_tile_kernel(const BwdPlan pl,
                                                                 const BwdBuffers bf) {
+  constexpr int NT = kTileThreads;
   constexpr int VB = VEC * EV::kBytes;
   constexpr int NC = 1 << DIM;
   constexpr int RW = DIM + 2;        // words per record
   constexpr int MI = kTileMaxItems;  // owner items per thread
+  constexpr int RPT = kTileRecPerThread;
+  constexpr int GPT = kTileGradPerThread;
   typedef typename EC::T TC;
   typedef typename EV::T TV;
   extern __shared__ __attribute__((aligned(16))) char s_mem[];
@@ -290,31 +570,15 @@ __global__ __launch_bounds__(kTileThreads) void bwd_tile_kernel(const BwdPlan pl
   const TileCoord tc = decode_tile(pl, t);
   const BwdLevel lv = pl.lv[tc.l];
 
-  char* s_val = s_mem;
-  char* s_g = s_mem + pl.lds_val_bytes;                                      // [S][C] raw rows
+  char* s_g = s_mem;                                                         // [S][C] raw rows
   uint2* s_ent = reinterpret_cast<uint2*>(s_g + pl.lds_g_bytes);             // [S * NC]
   uint32_t* s_rec = reinterpret_cast<uint32_t*>(s_ent + (size_t)pl.S * NC);  // [S][RW]
   uint32_t* s_cnt = s_rec + (size_t)pl.S * RW;                               // [rcells + 1]
-  uint32_t* s_cur = s_cnt + pl.rcells + 1;                                   // [rcells]
-  uint32_t* s_w = s_cur + pl.rcells;                                         // [waves]
+  uint32_t* s_w = s_cnt + pl.rcells + 1;                                     // [NT / 64]
   const int ncell_r = pl.rcells;
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc(bf.value, pl.value_bytes);
-  const uint32_t rs = (uint32_t)pl.H * (uint32_t)pl.C * EV::kBytes;  // bytes between rows of K
-  const uint32_t bh_base = ((tc.b * (uint32_t)pl.K) * (uint32_t)pl.H + tc.h) * (uint32_t)pl.C * EV::kBytes;
   const uint32_t grow = (uint32_t)pl.C * EV::kBytes;  // bytes of one staged grad_out row
-  const int LP = pl.L * pl.P;
-
-  // stage the value region [X0, X0+TX] x [Y0, Y0+TY] (x [Z0, Z0+TZ]); cells outside the
-  // level read as zero
-  for (int i = threadIdx.x; i < ncell_r * pl.nvec; i += kTileThreads) {
-    const int cell = i / pl.nvec, ch = i - cell * pl.nvec;
-    const int rx = cell % pl.RX, ry = (cell / pl.RX) % pl.RY, rz = cell / (pl.RX * pl.RY);
-    const int x = tc.X0 + rx, y = tc.Y0 + ry, z = tc.Z0 + rz;
-    const bool in = x < lv.W && y < lv.H && z < lv.D;
-    const uint32_t row = (uint32_t)lv.start + ((uint32_t)z * lv.H + y) * lv.W + x;
-    const RawVec<VB> r = buf_load<VB>(rv, in ? bh_base + row * rs + ch * VB : kOobOffset);
-    *reinterpret_cast<RawVec<VB>*>(s_val + cell * pl.val_row_bytes + ch * VB) = r;
-  }
+  const TV* gout = static_cast<const TV*>(bf.grad_out) + ((size_t)tc.b * pl.Q * pl.H + tc.h) * pl.C;
+  const size_t grad_q_stride = (size_t)pl.H * pl.C;  // elements between queries of grad_out
 
   float acc[MI][VEC];
 #pragma unroll
@@ -322,109 +586,76 @@ __global__ __launch_bounds__(kTileThreads) void bwd_tile_kernel(const BwdPlan pl
 #pragma unroll
     for (int k = 0; k < VEC; ++k) acc[m][k] = 0.0f;
 
-  const int lg = pl.lpu_log2;
-  const uint32_t lanes = 1u << lg;
-  const uint32_t grp = threadIdx.x >> lg;
-  const uint32_t lane = threadIdx.x & (lanes - 1u);
-  const bool act = (int)lane < pl.nvec;
-  const uint32_t groups = (uint32_t)kTileThreads >> lg;
-
   for (uint32_t sb = beg; sb < end; sb += pl.S) {
     const uint32_t nrec = min((uint32_t)pl.S, end - sb);
-    for (int i = threadIdx.x; i <= ncell_r; i += kTileThreads) s_cnt[i] = 0u;
-    __syncthreads();  // value region staged (first sub-batch); counters cleared
+    // A1. records -> LDS; clear the counters
+    for (uint32_t i = threadIdx.x; i < nrec * RW; i += NT) s_rec[i] = bf.records[(size_t)sb * RW + i];
+    for (int i = threadIdx.x; i <= ncell_r; i += NT) s_cnt[i] = 0u;
+    __syncthreads();
 
-    // A. record pass
-    for (uint32_t r = grp; r < nrec; r += groups) {
-      uint32_t rw[RW];
-      const uint32_t* grec = bf.records + (size_t)(sb + r) * RW;
+    // A2. grad_out rows -> LDS; corner counts and ranks
+    {
+      RawVec<VB> gr[GPT];
+      const uint32_t nchunk = nrec * (uint32_t)pl.nvec;
 #pragma unroll
-      for (int k = 0; k < RW; ++k) rw[k] = grec[k];
-      if (lane == 0) {
-#pragma unroll
-        for (int k = 0; k < RW; ++k) s_rec[r * RW + k] = rw[k];
-      }
-      const uint32_t qp = rw[0] & kRecIdMask;
-      const uint32_t q = fdiv(qp, pl.div_p), p = qp - q * (uint32_t)pl.P;
-      const size_t bqh = ((size_t)tc.b * pl.Q + q) * pl.H + tc.h;
-      const size_t si = bqh * LP + (size_t)tc.l * pl.P + p;
-      const Sample<DIM> sm = record_sample<DIM>(rw, lv);
-      float g[VEC];
-      if (act) {
-        const RawVec<VB> raw =
-            glb_load<VB>(static_cast<const TV*>(bf.grad_out) + bqh * pl.C + lane * VEC);
-        *reinterpret_cast<RawVec<VB>*>(s_g + r * grow + lane * VB) = raw;
-        widen<EV, VEC>(raw, g);
-      } else {
-#pragma unroll
-        for (int k = 0; k < VEC; ++k) g[k] = 0.0f;
-      }
-      // count the valid corners per region cell, one lane per corner
-      for (int cc = (int)lane; cc < NC; cc += (int)lanes) {
-        const int cell = region_cell(pl, sm.ax.i0 + (cc & 1) - tc.X0, sm.ay.i0 + ((cc >> 1) & 1) - tc.Y0,
-                                     DIM == 3 ? sm.az.i0 + ((cc >> 2) & 1) - tc.Z0 : 0);
-        if (corner_valid<DIM>(cc, sm) && cell >= 0) atomicAdd(&s_cnt[cell], 1u);
-      }
-      float dot[NC];
-#pragma unroll
-      for (int cc = 0; cc < NC; ++cc) {
-        const int cell = region_cell(pl, sm.ax.i0 + (cc & 1) - tc.X0, sm.ay.i0 + ((cc >> 1) & 1) - tc.Y0,
-                                     DIM == 3 ? sm.az.i0 + ((cc >> 2) & 1) - tc.Z0 : 0);
-        dot[cc] = 0.0f;
-        if (act && corner_valid<DIM>(cc, sm) && cell >= 0) {
-          const RawVec<VB> rwv =
-              *reinterpret_cast<const RawVec<VB>*>(s_val + cell * pl.val_row_bytes + lane * VB);
-          float v[VEC];
-          widen<EV, VEC>(rwv, v);
-          float d = 0.0f;
-#pragma unroll
-          for (int k = 0; k < VEC; ++k) d = __builtin_fmaf(g[k], v[k], d);
-          dot[cc] = d;
+      for (int k = 0; k < GPT; ++k) {
+        const uint32_t j = threadIdx.x + k * NT;
+        if (j < nchunk) {
+          const uint32_t r = fdiv(j, pl.div_nvec), ch = j - r * (uint32_t)pl.nvec;
+          const uint32_t q = fdiv(s_rec[r * RW] & kRecIdMask, pl.div_p);
+          gr[k] = glb_load<VB>(gout + (size_t)q * grad_q_stride + ch * VEC);
         }
       }
-      float s_attn, s_x, s_y, s_z;
-      corner_grads<DIM>(sm, dot, s_attn, s_x, s_y, s_z);
-      s_attn = group_sum(s_attn, lg);
-      s_x = group_sum(s_x, lg);
-      s_y = group_sum(s_y, lg);
-      if constexpr (DIM == 3) s_z = group_sum(s_z, lg);
-      if (lane == 0) {
-        const float a = __builtin_bit_cast(float, rw[RW - 1]);
-        static_cast<TC*>(bf.grad_attn)[si] = (TC)s_attn;
-        TC* gl = static_cast<TC*>(bf.grad_loc) + si * DIM;
-        gl[0] = (TC)(sm.ax.pass ? (a * s_x) * (float)lv.W : 0.0f);
-        gl[1] = (TC)(sm.ay.pass ? (a * s_y) * (float)lv.H : 0.0f);
-        if constexpr (DIM == 3) gl[2] = (TC)(sm.az.pass ? (a * s_z) * (float)lv.D : 0.0f);
+#pragma unroll
+      for (int k = 0; k < GPT; ++k) {
+        const uint32_t j = threadIdx.x + k * NT;
+        if (j < nchunk) {
+          const uint32_t r = fdiv(j, pl.div_nvec), ch = j - r * (uint32_t)pl.nvec;
+          *reinterpret_cast<RawVec<VB>*>(s_g + r * grow + ch * VB) = gr[k];
+        }
+      }
+    }
+    uint32_t rank[RPT][NC];
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+      const uint32_t r = threadIdx.x + k * NT;
+      if (r >= nrec) continue;
+      const Sample<DIM> sm = record_sample<DIM>(s_rec + r * RW, lv);
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc) {
+        const int cell = corner_cell<DIM>(pl, tc, sm, cc);
+        if (corner_valid<DIM>(cc, sm) && cell >= 0) rank[k][cc] = atomicAdd(&s_cnt[cell], 1u);
       }
     }
     __syncthreads();
 
-    // B. exclusive scan of the per-cell counts (rcells <= kTileThreads)
+    // B. exclusive scan of the per-cell counts (rcells <= 2 * NT)
     {
-      const uint32_t v = (int)threadIdx.x < ncell_r ? s_cnt[threadIdx.x] : 0u;
+      const int i0 = 2 * (int)threadIdx.x;
+      const uint32_t v0 = i0 < ncell_r ? s_cnt[i0] : 0u;
+      const uint32_t v1 = i0 + 1 < ncell_r ? s_cnt[i0 + 1] : 0u;
       uint32_t tot;
-      const uint32_t ex = block_excl_scan<kTileThreads>(v, s_w, &tot);
-      if ((int)threadIdx.x < ncell_r) {
-        s_cnt[threadIdx.x] = ex;
-        s_cur[threadIdx.x] = 0u;
-      }
+      const uint32_t ex = block_excl_scan<NT>(v0 + v1, s_w, &tot);
+      if (i0 < ncell_r) s_cnt[i0] = ex;
+      if (i0 + 1 < ncell_r) s_cnt[i0 + 1] = ex + v0;
       if (threadIdx.x == 0) s_cnt[ncell_r] = tot;
     }
     __syncthreads();
 
-    // C. entry pass: one thread per record
-    for (uint32_t r = threadIdx.x; r < nrec; r += kTileThreads) {
+    // C. place the entries
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+      const uint32_t r = threadIdx.x + k * NT;
+      if (r >= nrec) continue;
       const uint32_t* rw = s_rec + r * RW;
       const Sample<DIM> sm = record_sample<DIM>(rw, lv);
       const float a = __builtin_bit_cast(float, rw[RW - 1]);
 #pragma unroll
       for (int cc = 0; cc < NC; ++cc) {
-        const int cell = region_cell(pl, sm.ax.i0 + (cc & 1) - tc.X0, sm.ay.i0 + ((cc >> 1) & 1) - tc.Y0,
-                                     DIM == 3 ? sm.az.i0 + ((cc >> 2) & 1) - tc.Z0 : 0);
+        const int cell = corner_cell<DIM>(pl, tc, sm, cc);
         if (corner_valid<DIM>(cc, sm) && cell >= 0) {
-          const uint32_t pos = s_cnt[cell] + atomicAdd(&s_cur[cell], 1u);
           const float cw = corner_weight<DIM>(cc, sm) * a;
-          s_ent[pos] = make_uint2(__builtin_bit_cast(uint32_t, cw), r);
+          s_ent[s_cnt[cell] + rank[k][cc]] = make_uint2(__builtin_bit_cast(uint32_t, cw), r);
         }
       }
     }
@@ -433,16 +664,15 @@ __global__ __launch_bounds__(kTileThreads) void bwd_tile_kernel(const BwdPlan pl
     // D. owner pass: fp32 register accumulation per (region cell, channel chunk)
 #pragma unroll
     for (int m = 0; m < MI; ++m) {
-      const int it = (int)threadIdx.x + m * kTileThreads;
+      const int it = (int)threadIdx.x + m * NT;
       if (it < ncell_r * pl.nvec) {
-        const int cell = it / pl.nvec, ch = it - cell * pl.nvec;
+        const int cell = (int)fdiv((uint32_t)it, pl.div_nvec), ch = it - cell * pl.nvec;
         const uint32_t e0 = s_cnt[cell], e1 = s_cnt[cell + 1];
         for (uint32_t e = e0; e < e1; ++e) {
           const uint2 en = s_ent[e];
           const float cw = __builtin_bit_cast(float, en.x);
-          const RawVec<VB> raw = *reinterpret_cast<const RawVec<VB>*>(s_g + en.y * grow + ch * VB);
           float gv[VEC];
-          widen<EV, VEC>(raw, gv);
+          widen<EV, VEC>(*reinterpret_cast<const RawVec<VB>*>(s_g + en.y * grow + ch * VB), gv);
 #pragma unroll
           for (int k = 0; k < VEC; ++k) acc[m][k] = __builtin_fmaf(cw, gv[k], acc[m][k]);
         }
@@ -456,10 +686,11 @@ __global__ __launch_bounds__(kTileThreads) void bwd_tile_kernel(const BwdPlan pl
   // for the fold kernel
 #pragma unroll
   for (int m = 0; m < MI; ++m) {
-    const int it = (int)threadIdx.x + m * kTileThreads;
+    const int it = (int)threadIdx.x + m * NT;
     if (it >= ncell_r * pl.nvec) continue;
-    const int cell = it / pl.nvec, ch = it - cell * pl.nvec;
-    const int rx = cell % pl.RX, ry = (cell / pl.RX) % pl.RY, rz = cell / (pl.RX * pl.RY);
+    const int cell = (int)fdiv((uint32_t)it, pl.div_nvec), ch = it - cell * pl.nvec;
+    const int rz = (int)fdiv((uint32_t)cell, pl.div_rxy), rxy = cell - rz * pl.RX * pl.RY;
+    const int ry = (int)fdiv((uint32_t)rxy, pl.div_rx), rx = rxy - ry * pl.RX;
     const int x = tc.X0 + rx, y = tc.Y0 + ry, z = tc.Z0 + rz;
     if (x >= lv.W || y >= lv.H || z >= lv.D) continue;
     const bool owned = rx < pl.TX && ry < pl.TY && rz < pl.TZ;
@@ -489,11 +720,11 @@ __global__ __launch_bounds__(kBlock) void bwd_fold_kernel(const BwdPlan pl, cons
   const uint32_t nch = bf.chunk_off[t + 1] - off;
   const TileCoord tc = decode_tile(pl, t);
   const BwdLevel lv = pl.lv[tc.l];
-  const uint32_t tbase = t - (uint32_t)((tc.tz * lv.nty + tc.ty) * lv.ntx + tc.tx);
   TV* gv = static_cast<TV*>(bf.grad_value);
   for (int i = threadIdx.x; i < pl.cells * pl.nvec; i += kBlock) {
-    const int cell = i / pl.nvec, ch = i - cell * pl.nvec;
-    const int lx = cell % pl.TX, ly = (cell / pl.TX) % pl.TY, lz = cell / (pl.TX * pl.TY);
+    const int cell = (int)fdiv((uint32_t)i, pl.div_nvec), ch = i - cell * pl.nvec;
+    const int lz = (int)fdiv((uint32_t)cell, pl.div_txy), lxy = cell - lz * pl.TX * pl.TY;
+    const int ly = (int)fdiv((uint32_t)lxy, pl.div_tx), lx = lxy - ly * pl.TX;
     const int x = tc.X0 + lx, y = tc.Y0 + ly, z = tc.Z0 + lz;
     if (x >= lv.W || y >= lv.H || z >= lv.D) continue;
     const bool interior = lx > 0 && ly > 0 && (DIM == 2 || lz > 0);
@@ -512,7 +743,8 @@ __global__ __launch_bounds__(kBlock) void bwd_fold_kernel(const BwdPlan pl, cons
       if ((dx && (lx != 0 || tc.tx == 0)) || (dy && (ly != 0 || tc.ty == 0)) ||
           (dz && (lz != 0 || tc.tz == 0)))
         continue;
-      const uint32_t tn = tbase + (uint32_t)(((tc.tz - dz) * lv.nty + (tc.ty - dy)) * lv.ntx + (tc.tx - dx));
+      const int tibn = lv.tile_off + ((tc.tz - dz) * lv.nty + (tc.ty - dy)) * lv.ntx + (tc.tx - dx);
+      const uint32_t tn = tc.g * (uint32_t)pl.bins + (((uint32_t)tibn << pl.hg_log2) | tc.hsub);
       const int rn = ((lz + dz * pl.TZ) * pl.RY + (ly + dy * pl.TY)) * pl.RX + (lx + dx * pl.TX);
       const uint32_t noff = bf.chunk_off[tn], nn = bf.chunk_off[tn + 1] - noff;
       for (uint32_t j = 0; j < nn; ++j) {
@@ -532,14 +764,24 @@ hipError_t run_bwd_t(const BwdPlan& pl, const BwdBuffers& bf, hipStream_t s) {
   const uint32_t nbin_wg = (uint32_t)pl.groups * (uint32_t)pl.wgpg;
   const size_t hist_bytes = (size_t)pl.bins * sizeof(uint32_t);
   if (nbin_wg == 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((bwd_bin_kernel<DIM, EC, false>), dim3(nbin_wg), dim3(kBlock), hist_bytes, s,
-                     pl, bf);
+  if (pl.P == 4 && pl.coords_aligned)
+    hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 4>), dim3(nbin_wg), dim3(kGradThreads),
+                       hist_bytes, s, pl, bf);
+  else if (pl.P == 8 && pl.coords_aligned)
+    hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 8>), dim3(nbin_wg), dim3(kGradThreads),
+                       hist_bytes, s, pl, bf);
+  else
+    hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 0>), dim3(nbin_wg), dim3(kGradThreads),
+                       hist_bytes, s, pl, bf);
   if (pl.T == 0) return hipGetLastError();  // no cell in any level: grad_value is empty
-  hipLaunchKernelGGL(bwd_colscan_kernel, dim3((pl.T + kBlock - 1) / kBlock), dim3(kBlock), 0, s,
-                     pl, bf);
+  const uint32_t waves_per_block = kBlock / kWave;
+  hipLaunchKernelGGL(bwd_colscan_kernel, dim3((pl.T + waves_per_block - 1) / waves_per_block),
+                     dim3(kBlock), 0, s, pl, bf);
   hipLaunchKernelGGL(bwd_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, pl, bf);
-  hipLaunchKernelGGL((bwd_bin_kernel<DIM, EC, true>), dim3(nbin_wg), dim3(kBlock), 2 * hist_bytes,
-                     s, pl, bf);
+  const size_t fill_bytes = 2 * hist_bytes +
+                            (size_t)kFillStage * (DIM + 3) * sizeof(uint32_t) +
+                            (kBlock / kWave) * sizeof(uint32_t);
+  hipLaunchKernelGGL((bwd_fill_kernel<DIM, EC>), dim3(nbin_wg), dim3(kBlock), fill_bytes, s, pl, bf);
   hipLaunchKernelGGL((bwd_tile_kernel<DIM, EV, EC, VEC>), dim3(pl.grid_chunks),
                      dim3(kTileThreads), pl.lds_bytes, s, pl, bf);
   hipLaunchKernelGGL((bwd_fold_kernel<DIM, EV, VEC>), dim3(pl.T), dim3(kBlock), 0, s, pl, bf);

@@ -59,58 +59,6 @@ __device__ inline void stage_levels(const Params& p, Level* s_lvl) {
 
 }  // namespace
 
-// Raw storage for N elements of EC read with the widest aligned loads.
-template <typename EC, int N>
-struct CoordBlock {
-  static constexpr int kBytes = N * EC::kBytes;
-  static constexpr int kDwords = (kBytes + 3) / 4;
-  uint32_t d[kDwords];
-};
-
-template <typename EC, int N>
-__device__ inline void load_block(CoordBlock<EC, N>& b, const typename EC::T* p) {
-  constexpr int B = CoordBlock<EC, N>::kBytes;
-  if constexpr (B % 16 == 0) {
-#pragma unroll
-    for (int i = 0; i < B / 16; ++i) {
-      const u32x4 v = reinterpret_cast<const u32x4*>(p)[i];
-      b.d[4 * i] = v[0];
-      b.d[4 * i + 1] = v[1];
-      b.d[4 * i + 2] = v[2];
-      b.d[4 * i + 3] = v[3];
-    }
-  } else if constexpr (B % 8 == 0) {
-#pragma unroll
-    for (int i = 0; i < B / 8; ++i) {
-      const u32x2 v = reinterpret_cast<const u32x2*>(p)[i];
-      b.d[2 * i] = v[0];
-      b.d[2 * i + 1] = v[1];
-    }
-  } else if constexpr (B % 4 == 0) {
-#pragma unroll
-    for (int i = 0; i < B / 4; ++i) b.d[i] = reinterpret_cast<const uint32_t*>(p)[i];
-  } else {
-    const uint16_t* h = reinterpret_cast<const uint16_t*>(p);
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-      if (i & 1) b.d[i / 2] |= (uint32_t)h[i] << 16;
-      else b.d[i / 2] = h[i];
-    }
-  }
-}
-
-// Element i of a block as fp32.
-template <typename EC, int N>
-__device__ inline float block_elem(const CoordBlock<EC, N>& b, int i) {
-  if constexpr (EC::kBytes == 4) {
-    return __builtin_bit_cast(float, b.d[i]);
-  } else {
-    const uint32_t u = b.d[i / 2];
-    if constexpr (__is_same(EC, BF16)) return (i & 1) ? bf16hi(u) : bf16lo(u);
-    else return (i & 1) ? f16hi(u) : f16lo(u);
-  }
-}
-
 // Replaces the reference's _fwd_kernel_2d (src/msda_triton/triton/msda_2d.py:85-260) and
 // _fwd_kernel (src/msda_triton/triton/msda_3d.py:80-288). Writes (B, Q, H*C) in the value
 // dtype directly instead of an fp32 (B*H, Q, C) scratch plus permute (msda_2d.py:649-651).

@@ -9,8 +9,14 @@
 namespace msda {
 
 constexpr int kMaxLevels = 64;
-constexpr int kTileThreads = 1024;  // threads of the backward tile kernel
-constexpr int kTileMaxItems = 2;    // (cell, channel chunk) items owned per tile thread
+constexpr int kTileThreads = 512;     // threads of the backward tile kernel
+constexpr int kTileMaxItems = 2;      // (region cell, channel chunk) items per tile thread
+constexpr int kTileRecPerThread = 2;  // sub-batch records counted per tile thread (S <= 2*NT)
+constexpr int kTileGradPerThread = 4; // grad_out row chunks staged per tile thread
+constexpr int kTileWavesPerSimd = 4;  // tile-kernel occupancy target: two workgroups per CU
+constexpr int kFillStage = 2048;      // records staged in LDS per fill round
+constexpr int kGradThreads = 256;     // threads of the backward sample-gradient kernel
+constexpr int kGradRounds = 4;        // unit groups each of its threads handles in turn
 
 // Forward parameters for one launch over a contiguous range of batches. Pointers are
 // already offset to the first batch of the range; all in-kernel offsets are 32-bit.
@@ -61,7 +67,9 @@ constexpr uint32_t kRecPassZ = 1u << 29;
 struct BwdLevel {
   int32_t start, W, H, D;      // first row in K and extents (D = 1 in 2D)
   int32_t ntx, nty, ntz;       // tiles along x, y, z
-  int32_t tile_off;            // index of the level's first tile within a (b, h)
+  int32_t tile_off;            // index of the level's first tile within a (b, h); the
+                               // coarsest level comes first so its long chunks start early
+  int32_t ntiles;              // ntx * nty * ntz
 };
 
 struct BwdPlan {
@@ -69,24 +77,29 @@ struct BwdPlan {
   int32_t L, P, C, H, K;
   uint32_t Q;
   FastDiv div_p;               // divisor P (record id -> q, p)
-  int32_t TX, TY, TZ;          // owned cells per tile (TZ = 1 in 2D)
+  FastDiv div_lp;              // divisor L * P (sample index -> unit, sample)
+  int32_t TX, TY, TZ;          // owned cells per tile, powers of two (TZ = 1 in 2D)
+  int32_t tx_log2, ty_log2, tz_log2;
+  FastDiv div_nvec;            // divisor nvec (item -> cell, channel chunk)
+  FastDiv div_rx, div_rxy;     // divisors RX and RX * RY (region cell -> rx, ry, rz)
+  FastDiv div_tx, div_txy;     // divisors TX and TX * TY (owned cell -> lx, ly, lz)
   int32_t RX, RY, RZ;          // region: tile + 1 along each axis (RZ = 1 in 2D)
   int32_t cells;               // owned cells per tile: TX * TY * TZ
-  int32_t rcells;              // region cells per tile: RX * RY * RZ (<= kTileThreads)
+  int32_t rcells;              // region cells per tile: RX * RY * RZ (<= 2 * kTileThreads)
   int32_t tiles_per_bh;
   int32_t hg_log2;
   int32_t groups;              // (batches in launch) * H / HG
-  int32_t wgpg;                // bin-kernel workgroups per group
-  int32_t bins;                // HG * tiles_per_bh
+  int32_t upw;                 // units (b, q, h) per bin workgroup: kGradRounds * kGradThreads / lanes per unit
+  int32_t wgpg;                // bin workgroups per group: ceil(Q * HG / upw)
+  int32_t bins;                // tiles_per_bh * HG; bin = tile_in_bh * HG + head_in_group
   uint32_t T;                  // groups * bins: tiles of this launch
   uint32_t R;                  // records per chunk (multiple of S)
   uint32_t S;                  // records per LDS sub-batch of the tile kernel
   int32_t lpu_log2, nvec;
   int32_t clamp;
+  int32_t coords_aligned;      // loc and attn are 16-byte aligned: per-batch block loads allowed
   float lo_g, hi_g;
   uint32_t value_bytes;
-  uint32_t val_row_bytes;      // LDS stride of a staged value row
-  uint32_t lds_val_bytes;      // bytes of the staged value region
   uint32_t lds_g_bytes;        // bytes of the staged grad_out rows of a sub-batch
   uint32_t lds_bytes;          // total dynamic LDS of the tile kernel
   uint32_t max_chunks;         // upper bound of the chunk count
@@ -101,7 +114,7 @@ struct BwdBuffers {
   void* grad_value;
   void* grad_loc;
   void* grad_attn;
-  uint32_t* counts;      // groups * wgpg * bins: per-(bin workgroup, bin) counts -> offsets
+  uint32_t* counts;      // (groups * bins) x wgpg: per-(tile, bin workgroup) counts -> offsets
   uint32_t* bin_start;   // T + 1: record totals -> first record of each tile
   uint32_t* chunk_off;   // T + 1: first chunk of each tile; [T] = number of chunks
   uint32_t* chunk_tile;  // max_chunks: tile of each chunk

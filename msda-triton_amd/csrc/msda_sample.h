@@ -24,10 +24,10 @@ struct Axis {
   bool pass;    // gradient passes the grid clamp (backward mask of torch.clamp)
 };
 
-// Tile (along one axis, extent T cells) that owns a sample's lowest valid corner; the
-// sample must have a valid corner on this axis (i0 >= -1). Its corners i0 and i0 + 1
-// then lie in [tile * T - 1, tile * T + T]: the tile or its one-cell high-side halo.
-__device__ inline int anchor_tile(const Axis& a, int T) { return (a.i0 < 0 ? 0 : a.i0) / T; }
+// Tile (along one axis, extent T = 2^t_log2 cells) that owns a sample's lowest valid
+// corner; the sample must have a valid corner on this axis (i0 >= -1). Its corners i0 and
+// i0 + 1 then lie in [tile * T - 1, tile * T + T]: the tile or its one-cell high-side halo.
+__device__ inline int anchor_tile(const Axis& a, int t_log2) { return (a.i0 < 0 ? 0 : a.i0) >> t_log2; }
 
 // Pixel coordinate u of one location component; *pass is false where the grid clamp
 // was active.
@@ -129,6 +129,94 @@ __device__ inline void corner_grads(const Sample<DIM>& sm, const float* dot, flo
       s_x += sx * wy * dot[c];
       s_y += wx * sy * dot[c];
     }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Coordinate / weight blocks: the N consecutive coordinate-type elements of a batch of
+// samples, read with the widest loads their alignment allows (callers guarantee the
+// block start is aligned to the block size, up to 16 bytes).
+template <typename EC, int N>
+struct CoordBlock {
+  static constexpr int kBytes = N * EC::kBytes;
+  static constexpr int kDwords = (kBytes + 3) / 4;
+  uint32_t d[kDwords];
+};
+
+template <typename EC, int N>
+__device__ inline void load_block(CoordBlock<EC, N>& b, const typename EC::T* p) {
+  constexpr int B = CoordBlock<EC, N>::kBytes;
+  if constexpr (B % 16 == 0) {
+#pragma unroll
+    for (int i = 0; i < B / 16; ++i) {
+      const u32x4 v = reinterpret_cast<const u32x4*>(p)[i];
+      b.d[4 * i] = v[0];
+      b.d[4 * i + 1] = v[1];
+      b.d[4 * i + 2] = v[2];
+      b.d[4 * i + 3] = v[3];
+    }
+  } else if constexpr (B % 8 == 0) {
+#pragma unroll
+    for (int i = 0; i < B / 8; ++i) {
+      const u32x2 v = reinterpret_cast<const u32x2*>(p)[i];
+      b.d[2 * i] = v[0];
+      b.d[2 * i + 1] = v[1];
+    }
+  } else if constexpr (B % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < B / 4; ++i) b.d[i] = reinterpret_cast<const uint32_t*>(p)[i];
+  } else {
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(p);
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      if (i & 1) b.d[i / 2] |= (uint32_t)h[i] << 16;
+      else b.d[i / 2] = h[i];
+    }
+  }
+}
+
+// Store N fp32 values as a block of EC elements (round to nearest even), with the widest
+// stores the alignment allows.
+template <typename EC, int N>
+__device__ inline void store_block(typename EC::T* p, const float (&v)[N]) {
+  constexpr int B = N * EC::kBytes;
+  uint32_t d[(B + 3) / 4];
+  if constexpr (EC::kBytes == 4) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) d[i] = __builtin_bit_cast(uint32_t, v[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < (N + 1) / 2; ++i) {
+      const uint32_t lo = __builtin_bit_cast(uint16_t, narrow<EC>(v[2 * i]));
+      const uint32_t hi = 2 * i + 1 < N ? __builtin_bit_cast(uint16_t, narrow<EC>(v[2 * i + 1])) : 0u;
+      d[i] = lo | (hi << 16);
+    }
+  }
+  if constexpr (B % 16 == 0) {
+#pragma unroll
+    for (int i = 0; i < B / 16; ++i)
+      reinterpret_cast<u32x4*>(p)[i] = u32x4{d[4 * i], d[4 * i + 1], d[4 * i + 2], d[4 * i + 3]};
+  } else if constexpr (B % 8 == 0) {
+#pragma unroll
+    for (int i = 0; i < B / 8; ++i) reinterpret_cast<u32x2*>(p)[i] = u32x2{d[2 * i], d[2 * i + 1]};
+  } else if constexpr (B % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < B / 4; ++i) reinterpret_cast<uint32_t*>(p)[i] = d[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) p[i] = narrow<EC>(v[i]);
+  }
+}
+
+// Element i of a block as fp32.
+template <typename EC, int N>
+__device__ inline float block_elem(const CoordBlock<EC, N>& b, int i) {
+  if constexpr (EC::kBytes == 4) {
+    return __builtin_bit_cast(float, b.d[i]);
+  } else {
+    const uint32_t u = b.d[i / 2];
+    if constexpr (__is_same(EC, BF16)) return (i & 1) ? bf16hi(u) : bf16lo(u);
+    else return (i & 1) ? f16hi(u) : f16lo(u);
   }
 }
 
