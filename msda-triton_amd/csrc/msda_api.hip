@@ -37,6 +37,7 @@ const char* dtype_name(int dt) {
 }
 
 constexpr uint64_t kLim31 = 0x7FFFFFFFull;
+constexpr uint64_t kCus = 256;  // MI355X compute units: workgroups of the staged forward
 constexpr uint32_t kChunkRecords = 4096;        // records per tile-kernel chunk (rounded to S)
 constexpr uint32_t kTileLdsTarget = 52 * 1024;  // three tile workgroups per CU (160 KB LDS)
 constexpr uint32_t kTileLdsBudget = 160 * 1024 - 256;  // one workgroup per CU
@@ -388,8 +389,10 @@ int msda_fwd(const msda_desc* d, const void* value, const int32_t* spatial_shape
   const void* vptrs[2] = {value, output};
   Layout lay;
   if ((rc = choose_layout(d, vptrs, 2, &lay))) return rc;
-  msda::LaunchFn fn = msda::get_fwd_launcher(d->dim, d->value_dtype, d->coord_dtype, lay.vec_bytes);
-  if (!fn) return fail(MSDA_ERR_DTYPE, "no forward kernel for this dtype combination");
+  msda::LaunchFn fn = msda::get_fwd_launcher(d->dim, d->value_dtype, d->coord_dtype, lay.vec_bytes, false);
+  msda::LaunchFn fn_staged =
+      msda::get_fwd_launcher(d->dim, d->value_dtype, d->coord_dtype, lay.vec_bytes, true);
+  if (!fn || !fn_staged) return fail(MSDA_ERR_DTYPE, "no forward kernel for this dtype combination");
 
   const int64_t nb = batches_per_launch(d, lay);
   const int sv = elem_bytes(d->value_dtype), sc = elem_bytes(d->coord_dtype);
@@ -407,7 +410,19 @@ int msda_fwd(const msda_desc* d, const void* value, const int32_t* spatial_shape
     p.shapes = spatial_shapes;
     p.starts = level_start;
     p.coords_aligned = aligned(p.loc, 16) && aligned(p.attn, 16);
-    hipError_t e = fn(p, static_cast<hipStream_t>(stream));
+    // Staged kernel: one workgroup per CU, each (batch, head) slice split into query
+    // ranges; used when every workgroup gets enough queries to amortise its LDS copy.
+    const uint64_t slices = (uint64_t)bc * d->num_heads;
+    const uint64_t splits = (kCus + slices - 1) / slices;
+    const uint64_t qper = ((uint64_t)d->num_queries + splits - 1) / splits;
+    const bool staged = has_samples && qper >= msda::kFwdStageMinQueries;
+    if (staged) {
+      p.splits = (uint32_t)splits;
+      p.qper = (uint32_t)qper;
+      p.stage_bytes = msda::kFwdStageLds;
+      p.nblocks = (uint32_t)(slices * splits);
+    }
+    hipError_t e = (staged ? fn_staged : fn)(p, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(MSDA_ERR_HIP, "msda_fwd launch failed: %s", hipGetErrorString(e));
   }
   return MSDA_OK;

@@ -116,6 +116,12 @@ __device__ inline uint32_t raw_dword(const RawVec<NBYTES>& r, int i) {
   else return (uint32_t)r.v;
 }
 
+// Reinterpret a 32-bit word as fp32 and back. The argument is taken by value: clang's
+// __builtin_bit_cast applied directly to an element of an ext_vector_type value reads the
+// vector's first element whatever the index, so vector elements must pass through these.
+__device__ inline float as_float(uint32_t u) { return __builtin_bit_cast(float, u); }
+__device__ inline uint32_t as_u32(float f) { return __builtin_bit_cast(uint32_t, f); }
+
 __device__ inline float bf16lo(uint32_t u) { return __builtin_bit_cast(float, u << 16); }
 __device__ inline float bf16hi(uint32_t u) { return __builtin_bit_cast(float, u & 0xffff0000u); }
 __device__ inline float f16lo(uint32_t u) {
@@ -159,8 +165,10 @@ __device__ inline typename E::T narrow(float x) {
 template <typename E, int VEC>
 __device__ inline void store_vec(typename E::T* p, const float (&a)[VEC]) {
   if constexpr (E::kBytes == 4) {
-    if constexpr (VEC == 4) {
-      *reinterpret_cast<float4*>(p) = make_float4(a[0], a[1], a[2], a[3]);
+    if constexpr (VEC % 4 == 0) {
+#pragma unroll
+      for (int i = 0; i < VEC; i += 4)
+        *reinterpret_cast<float4*>(p + i) = make_float4(a[i], a[i + 1], a[i + 2], a[i + 3]);
     } else if constexpr (VEC == 2) {
       *reinterpret_cast<float2*>(p) = make_float2(a[0], a[1]);
     } else {

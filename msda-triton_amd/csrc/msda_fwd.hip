@@ -1,17 +1,25 @@
-// msda_fwd.hip — gfx950 forward kernel: bilinear (2D) / trilinear (3D) multi-scale
+// msda_fwd.hip — gfx950 forward kernels: bilinear (2D) / trilinear (3D) multi-scale
 // deformable attention.
 //
 // Work decomposition. A "unit" is one (batch b, query q, head h), owned by an aligned
 // group of 2^lpu_log2 lanes of one wave64. Lane j of the group holds channels
 // [j*VEC, (j+1)*VEC), so each corner of a sample is one VEC*sizeof(value)-byte load per
 // lane (16 B when C allows) and the group together reads one contiguous C-channel value
-// row. Units are enumerated in (b, head-group, q, head-in-group) order so the heads that
-// share 128-byte lines of value/loc/attn/output rows run side by side, and workgroups are
-// remapped so each XCD owns a contiguous unit range, keeping a (batch, head-group) value
-// slice resident in that XCD's L2. Samples are processed in batches of SB: all SB*2^DIM
-// corner loads of a batch are issued before any is consumed, which keeps 16 row loads in
-// flight per lane. Corners outside the level read as zero through the buffer range check;
-// accumulation is fp32 and the output is rounded once to the value dtype.
+// row. Samples are processed in batches of SB: all SB*2^DIM corner loads of a batch are
+// issued before any is consumed, which keeps 16 row loads in flight per lane. Accumulation
+// is fp32 and the output is rounded once to the value dtype.
+//
+// Two kernels share that per-unit code:
+//  * msda_fwd_kernel: units in (b, head-group, q, head-in-group) order so the heads that
+//    share 128-byte lines of loc/attn/output run side by side; workgroups remapped so each
+//    XCD owns a contiguous unit range and keeps a (batch, head-group) value slice in its
+//    L2. Corners outside the level read as zero through the buffer range check.
+//  * msda_fwd_staged_kernel: one 1024-thread workgroup per CU serves one (batch, head) and
+//    a range of queries. It first copies the smallest levels of that (batch, head) value
+//    slice that fit kFwdStageLds into LDS; corners on those levels are then read from LDS,
+//    the others from L2 (their slices again XCD-resident). Every row gather goes to L2 as a
+//    full 128-byte line of which one head uses 64 bytes, so serving the coarse levels from
+//    LDS removes their share of the L2 line traffic, which bounds this kernel.
 #include "msda_internal.h"
 #include "msda_sample.h"
 
@@ -41,7 +49,7 @@ __device__ inline bool decode_unit(const Params& p, Unit& u) {
 
 template <int DIM>
 __device__ inline void stage_levels(const Params& p, Level* s_lvl) {
-  for (int i = threadIdx.x; i < p.L; i += kBlock) {
+  for (int i = threadIdx.x; i < p.L; i += blockDim.x) {
     Level e;
     e.start = p.starts[i];
     if constexpr (DIM == 2) {
@@ -57,90 +65,134 @@ __device__ inline void stage_levels(const Params& p, Level* s_lvl) {
   }
 }
 
-}  // namespace
+// Corner rows of a batch of samples: from the global value slice through the buffer range
+// check (zero outside the level), or, for a level held in LDS, from its staged rows (zero
+// outside the level by selection).
+template <int DIM, int VB, int SB, bool LDS>
+__device__ inline void fetch_rows(const Sample<DIM> (&sm)[SB], const Level& lv,
+                                  __amdgpu_buffer_rsrc_t rv, uint32_t vbase, uint32_t rs,
+                                  const char* s_rows, int32_t lrow, uint32_t lane_off,
+                                  RawVec<VB> (&raw)[SB][1 << DIM]) {
+  constexpr int NC = 1 << DIM;
+  const uint32_t W = (uint32_t)lv.W, HW = (uint32_t)lv.W * (uint32_t)lv.H;
+#pragma unroll
+  for (int k = 0; k < SB; ++k) {
+    uint32_t row0 = (uint32_t)sm[k].ay.i0 * W + (uint32_t)sm[k].ax.i0;
+    if constexpr (DIM == 3) row0 += (uint32_t)sm[k].az.i0 * HW;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const uint32_t dr = ((c & 1) ? 1u : 0u) + ((c & 2) ? W : 0u) + ((DIM == 3 && (c & 4)) ? HW : 0u);
+      const bool ok = corner_valid<DIM>(c, sm[k]);
+      if constexpr (LDS) {
+        // row stride of the staged slice is rs (= C * element size) as well
+        const uint32_t off = ok ? ((uint32_t)lrow + row0 + dr) * rs + lane_off : lane_off;
+        RawVec<VB> v = *reinterpret_cast<const RawVec<VB>*>(s_rows + off);
+        if constexpr (VB >= 4) {
+#pragma unroll
+          for (int i = 0; i < VB / 4; ++i) {
+            if constexpr (VB == 4) v.v = ok ? v.v : 0u;
+            else v.v[i] = ok ? v.v[i] : 0u;
+          }
+        } else {
+          v.v = ok ? v.v : (uint16_t)0;
+        }
+        raw[k][c] = v;
+      } else {
+        raw[k][c] = buf_load<VB>(rv, ok ? vbase + ((uint32_t)lv.start + row0 + dr) * rs : kOobOffset);
+      }
+    }
+  }
+}
 
-// Replaces the reference's _fwd_kernel_2d (src/msda_triton/triton/msda_2d.py:85-260) and
-// _fwd_kernel (src/msda_triton/triton/msda_3d.py:80-288). Writes (B, Q, H*C) in the value
-// dtype directly instead of an fp32 (B*H, Q, C) scratch plus permute (msda_2d.py:649-651).
+// The whole forward of one unit: sum over levels and points of attn * sample(value).
 //
-// PT > 0: the number of points per level is a compile-time constant. Each level's PT*DIM
-// coordinates and PT weights are fetched as one contiguous block per lane, the next
-// level's block is fetched while this level's corner rows are in flight, and all corner
-// rows of a level (in batches of SB samples) are issued before any is consumed; the
-// in-order completion of vector loads then never makes a coordinate load wait behind a
-// row gather. PT == 0 handles any P with per-sample loads.
-template <int DIM, typename EV, typename EC, int VEC, int PT>
-__global__ __launch_bounds__(kBlock) void msda_fwd_kernel(const Params p) {
+// PT > 0: the number of points per level is a compile-time constant; every coordinate and
+// weight block of the unit is loaded before its first row gather, and all corner rows of a
+// batch are issued before any is consumed. Used when the unit's blocks fit kFwdCoordSlots<DIM>
+// per lane (L * P / SB <= kFwdCoordSlots * nvec). PT == 0 handles any P with per-sample
+// loads.
+//
+// STAGED: s_loff[l] >= 0 gives the first LDS row of level l in s_rows (rows of rs bytes).
+template <int DIM, typename EV, typename EC, int VEC, int PT, bool STAGED>
+__device__ inline void unit_forward(const Params& p, const Level* s_lvl, const int32_t* s_loff,
+                                    const char* s_rows, uint32_t b, uint32_t h, uint32_t bqh,
+                                    uint32_t lane, float (&acc)[VEC]) {
   constexpr int VB = VEC * EV::kBytes;
   constexpr int NC = 1 << DIM;
   constexpr int SB = PT > 0 ? (DIM == 2 ? (PT < 4 ? PT : 4) : (PT < 2 ? PT : 2)) : (DIM == 2 ? 4 : 2);
   typedef typename EC::T TC;
-  __shared__ Level s_lvl[kMaxLevels];
-  stage_levels<DIM>(p, s_lvl);
-  __syncthreads();
-
-  Unit u;
-  if (!decode_unit(p, u)) return;
-  if ((int)u.lane >= p.nvec) return;
-
   const int LP = p.L * p.P;
-  const TC* locp = static_cast<const TC*>(p.loc) + (size_t)u.bqh * (LP * DIM);
-  const TC* attp = static_cast<const TC*>(p.attn) + (size_t)u.bqh * LP;
+  const TC* locp = static_cast<const TC*>(p.loc) + (size_t)bqh * (LP * DIM);
+  const TC* attp = static_cast<const TC*>(p.attn) + (size_t)bqh * LP;
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.value, p.value_bytes);
   const uint32_t rs = (uint32_t)p.H * (uint32_t)p.C * EV::kBytes;  // bytes between rows of K
-  const uint32_t vbase =
-      ((u.b * (uint32_t)p.K * (uint32_t)p.H + u.h) * (uint32_t)p.C + u.lane * VEC) * EV::kBytes;
+  const uint32_t lane_off = lane * VB;
+  const uint32_t vbase = ((b * (uint32_t)p.K * (uint32_t)p.H + h) * (uint32_t)p.C) * EV::kBytes + lane_off;
+  const uint32_t lrs = (uint32_t)p.C * EV::kBytes;  // bytes per staged row
 
-  float acc[VEC];
 #pragma unroll
   for (int i = 0; i < VEC; ++i) acc[i] = 0.0f;
 
   if constexpr (PT > 0) {
-    // Software pipeline over batches of SB samples (all levels, in order): the batch's
-    // coordinates and weights were fetched during the previous iteration.
+    // The unit's coordinate and weight blocks (one per batch of SB samples) are fetched
+    // up front, spread over its lanes: lane j holds batches j, j + nvec, ... With one
+    // independent load per lane and slot, no batch waits on a coordinate load; each batch
+    // broadcasts its block from the holding lane (ds_bpermute within the lane group).
     constexpr int BPL = PT / SB;  // batches per level
-    CoordBlock<EC, SB * DIM> lb;
-    CoordBlock<EC, SB> ab;
+    constexpr int LW = CoordBlock<EC, SB * DIM>::kDwords, AW = CoordBlock<EC, SB>::kDwords;
     const int nbatch = p.L * BPL;
-    if (nbatch > 0) {
-      load_block<EC, SB * DIM>(lb, locp);
-      load_block<EC, SB>(ab, attp);
+    const int nv = p.nvec;
+    CoordBlock<EC, SB * DIM> hl[kFwdCoordSlots<DIM>];
+    CoordBlock<EC, SB> ha[kFwdCoordSlots<DIM>];
+#pragma unroll
+    for (int sl = 0; sl < kFwdCoordSlots<DIM>; ++sl) {
+      const int bj = (int)lane + sl * nv;
+      if (bj < nbatch) {
+        load_block<EC, SB * DIM>(hl[sl], locp + bj * (SB * DIM));
+        load_block<EC, SB>(ha[sl], attp + bj * SB);
+      }
     }
+    const int gbase = (int)(__lane_id() & ~((1u << p.lpu_log2) - 1u));  // first lane of the group
 #pragma unroll 1
     for (int bi = 0; bi < nbatch; ++bi) {
-      const Level lv = s_lvl[bi / BPL];
-      const uint32_t W = (uint32_t)lv.W, HW = (uint32_t)lv.W * (uint32_t)lv.H;
-      uint32_t off[SB][NC];
+      const int l = bi / BPL;
+      const Level lv = s_lvl[l];
+      const int sl = bi / nv;
+      const int src = (gbase + (bi - sl * nv)) << 2;
+      CoordBlock<EC, SB * DIM> lb;
+      CoordBlock<EC, SB> ab;
+#pragma unroll
+      for (int w = 0; w < LW; ++w) {
+        uint32_t x = hl[0].d[w];
+#pragma unroll
+        for (int k = 1; k < kFwdCoordSlots<DIM>; ++k) x = sl == k ? hl[k].d[w] : x;
+        lb.d[w] = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)x);
+      }
+#pragma unroll
+      for (int w = 0; w < AW; ++w) {
+        uint32_t x = ha[0].d[w];
+#pragma unroll
+        for (int k = 1; k < kFwdCoordSlots<DIM>; ++k) x = sl == k ? ha[k].d[w] : x;
+        ab.d[w] = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)x);
+      }
+      Sample<DIM> sm[SB];
       float cw[SB][NC];
 #pragma unroll
       for (int k = 0; k < SB; ++k) {
-        Sample<DIM> sm;
-        sm.ax = make_axis(block_elem(lb, k * DIM + 0), (float)lv.W, lv.W, p.clamp, p.lo_g, p.hi_g);
-        sm.ay = make_axis(block_elem(lb, k * DIM + 1), (float)lv.H, lv.H, p.clamp, p.lo_g, p.hi_g);
-        uint32_t row0 = (uint32_t)lv.start + (uint32_t)sm.ay.i0 * W + (uint32_t)sm.ax.i0;
-        if constexpr (DIM == 3) {
-          sm.az = make_axis(block_elem(lb, k * DIM + 2), (float)lv.D, lv.D, p.clamp, p.lo_g, p.hi_g);
-          row0 += (uint32_t)sm.az.i0 * HW;
-        }
+        sm[k].ax = make_axis(block_elem(lb, k * DIM + 0), (float)lv.W, lv.W, p.clamp, p.lo_g, p.hi_g);
+        sm[k].ay = make_axis(block_elem(lb, k * DIM + 1), (float)lv.H, lv.H, p.clamp, p.lo_g, p.hi_g);
+        if constexpr (DIM == 3)
+          sm[k].az = make_axis(block_elem(lb, k * DIM + 2), (float)lv.D, lv.D, p.clamp, p.lo_g, p.hi_g);
         const float a = block_elem(ab, k);
-        const uint32_t off0 = vbase + row0 * rs;
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          const uint32_t dr = ((c & 1) ? 1u : 0u) + ((c & 2) ? W : 0u) + ((DIM == 3 && (c & 4)) ? HW : 0u);
-          off[k][c] = corner_valid<DIM>(c, sm) ? off0 + dr * rs : kOobOffset;
-          cw[k][c] = corner_weight<DIM>(c, sm) * a;
-        }
+        for (int c = 0; c < NC; ++c) cw[k][c] = corner_weight<DIM>(c, sm[k]) * a;
       }
       RawVec<VB> raw[SB][NC];
-#pragma unroll
-      for (int k = 0; k < SB; ++k)
-#pragma unroll
-        for (int c = 0; c < NC; ++c) raw[k][c] = buf_load<VB>(rv, off[k][c]);
-      if (bi + 1 < nbatch) {
-        // next batch's coordinates and weights, queued behind this batch's rows
-        load_block<EC, SB * DIM>(lb, locp + (bi + 1) * (SB * DIM));
-        load_block<EC, SB>(ab, attp + (bi + 1) * SB);
-      }
+      const int32_t lrow = STAGED ? s_loff[l] : -1;
+      if (STAGED && lrow >= 0)
+        fetch_rows<DIM, VB, SB, true>(sm, lv, rv, vbase, lrs, s_rows, lrow, lane_off, raw);
+      else
+        fetch_rows<DIM, VB, SB, false>(sm, lv, rv, vbase, rs, s_rows, lrow, lane_off, raw);
 #pragma unroll
       for (int k = 0; k < SB; ++k) {
 #pragma unroll
@@ -155,28 +207,24 @@ __global__ __launch_bounds__(kBlock) void msda_fwd_kernel(const Params p) {
   } else {
     for (int l = 0; l < p.L; ++l) {
       const Level lv = s_lvl[l];
-      const uint32_t W = (uint32_t)lv.W, HW = (uint32_t)lv.W * (uint32_t)lv.H;
+      const int32_t lrow = STAGED ? s_loff[l] : -1;
       for (int p0 = 0; p0 < p.P; p0 += SB) {
-        RawVec<VB> raw[SB][NC];
+        Sample<DIM> sm[SB];
         float cw[SB][NC];
 #pragma unroll
         for (int k = 0; k < SB; ++k) {
           const int s = l * p.P + p0 + k;
           const bool live = p0 + k < p.P;
           const float a = live ? (float)attp[s] : 0.0f;
-          const Sample<DIM> sm =
-              make_sample<DIM>(locp + (live ? s : 0) * DIM, lv, p.clamp, p.lo_g, p.hi_g);
-          uint32_t row0 = (uint32_t)lv.start + (uint32_t)sm.ay.i0 * W + (uint32_t)sm.ax.i0;
-          if constexpr (DIM == 3) row0 += (uint32_t)sm.az.i0 * HW;
-          const uint32_t off0 = vbase + row0 * rs;
+          sm[k] = make_sample<DIM>(locp + (live ? s : 0) * DIM, lv, p.clamp, p.lo_g, p.hi_g);
 #pragma unroll
-          for (int c = 0; c < NC; ++c) {
-            const uint32_t dr = ((c & 1) ? 1u : 0u) + ((c & 2) ? W : 0u) +
-                                ((DIM == 3 && (c & 4)) ? HW : 0u);
-            raw[k][c] = buf_load<VB>(rv, (live && corner_valid<DIM>(c, sm)) ? off0 + dr * rs : kOobOffset);
-            cw[k][c] = corner_weight<DIM>(c, sm) * a;
-          }
+          for (int c = 0; c < NC; ++c) cw[k][c] = corner_weight<DIM>(c, sm[k]) * a;
         }
+        RawVec<VB> raw[SB][NC];
+        if (STAGED && lrow >= 0)
+          fetch_rows<DIM, VB, SB, true>(sm, lv, rv, vbase, lrs, s_rows, lrow, lane_off, raw);
+        else
+          fetch_rows<DIM, VB, SB, false>(sm, lv, rv, vbase, rs, s_rows, lrow, lane_off, raw);
 #pragma unroll
         for (int k = 0; k < SB; ++k) {
 #pragma unroll
@@ -193,49 +241,187 @@ __global__ __launch_bounds__(kBlock) void msda_fwd_kernel(const Params p) {
       }
     }
   }
+}
+
+}  // namespace
+
+// Replaces the reference's _fwd_kernel_2d (src/msda_triton/triton/msda_2d.py:85-260) and
+// _fwd_kernel (src/msda_triton/triton/msda_3d.py:80-288). Writes (B, Q, H*C) in the value
+// dtype directly instead of an fp32 (B*H, Q, C) scratch plus permute (msda_2d.py:649-651).
+template <int DIM, typename EV, typename EC, int VEC, int PT>
+__global__ __launch_bounds__(kBlock) void msda_fwd_kernel(const Params p) {
+  __shared__ Level s_lvl[kMaxLevels];
+  stage_levels<DIM>(p, s_lvl);
+  __syncthreads();
+  Unit u;
+  if (!decode_unit(p, u)) return;
+  if ((int)u.lane >= p.nvec) return;
+  float acc[VEC];
+  unit_forward<DIM, EV, EC, VEC, PT, false>(p, s_lvl, nullptr, nullptr, u.b, u.h, u.bqh, u.lane, acc);
   typename EV::T* outp = static_cast<typename EV::T*>(p.out) + (size_t)u.bqh * p.C + u.lane * VEC;
   store_vec<EV, VEC>(outp, acc);
 }
 
+// Same result as msda_fwd_kernel; the smallest levels of the workgroup's (batch, head)
+// value slice are read from LDS.
+template <int DIM, typename EV, typename EC, int VEC, int PT>
+__global__ __launch_bounds__(kFwdStageThreads) void msda_fwd_staged_kernel(const Params p) {
+  constexpr int NT = kFwdStageThreads;
+  constexpr int VB = VEC * EV::kBytes;
+  extern __shared__ __attribute__((aligned(16))) char s_rows[];
+  __shared__ Level s_lvl[kMaxLevels];
+  __shared__ int32_t s_loff[kMaxLevels];  // first LDS row of a staged level, else -1
+  __shared__ int32_t s_order[kMaxLevels];  // staged levels in LDS order
+  __shared__ uint32_t s_pfx[kMaxLevels + 1];  // their first piece in the flat staging index
+  __shared__ int32_t s_nst;
+  stage_levels<DIM>(p, s_lvl);
+  __syncthreads();
+  const uint32_t lrs = (uint32_t)p.C * EV::kBytes;  // bytes per staged row
+  const uint32_t nvec = (uint32_t)p.nvec;
+  if (threadIdx.x == 0) {
+    // greedy: smallest levels first, while they fit
+    const uint32_t cap = p.stage_bytes / lrs;
+    uint32_t used = 0;
+    int n = 0;
+    for (int l = 0; l < p.L; ++l) s_loff[l] = -1;
+    for (;;) {
+      int best = -1;
+      uint32_t bsz = 0;
+      for (int l = 0; l < p.L; ++l) {
+        if (s_loff[l] >= 0) continue;
+        const uint32_t sz = (uint32_t)s_lvl[l].W * (uint32_t)s_lvl[l].H * (uint32_t)s_lvl[l].D;
+        if (sz == 0 || used + sz > cap) continue;
+        if (best < 0 || sz < bsz) {
+          best = l;
+          bsz = sz;
+        }
+      }
+      if (best < 0) break;
+      s_loff[best] = (int32_t)used;
+      s_order[n] = best;
+      s_pfx[n] = used * nvec;
+      used += bsz;
+      ++n;
+    }
+    s_pfx[n] = used * nvec;
+    s_nst = n;
+  }
+  __syncthreads();
+
+  const uint32_t lb = xcd_logical_block(blockIdx.x, p.nblocks);
+  const uint32_t bh = lb / p.splits, split = lb - bh * p.splits;
+  const uint32_t b = bh / (uint32_t)p.H, h = bh - b * (uint32_t)p.H;
+  const uint32_t q0 = split * p.qper;
+  const uint32_t q1 = min(p.Q, q0 + p.qper);
+
+  // copy the staged levels' rows of (b, h): every load of a thread is issued before any of
+  // its stores
+  {
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.value, p.value_bytes);
+    const uint32_t rs = (uint32_t)p.H * (uint32_t)p.C * EV::kBytes;
+    const uint32_t vrow0 = ((b * (uint32_t)p.K * (uint32_t)p.H + h) * (uint32_t)p.C) * EV::kBytes;
+    const int nst = s_nst;
+    const uint32_t total = s_pfx[nst];
+    constexpr int KB = 8;
+    for (uint32_t i0 = threadIdx.x; i0 < total; i0 += KB * NT) {
+      RawVec<VB> v[KB];
+      uint32_t dst[KB];
+#pragma unroll
+      for (int k = 0; k < KB; ++k) {
+        const uint32_t i = i0 + (uint32_t)k * NT;
+        uint32_t goff = kOobOffset;
+        dst[k] = 0xffffffffu;
+        if (i < total) {
+          int j = 0;
+          while (j + 1 < nst && s_pfx[j + 1] <= i) ++j;
+          const uint32_t rel = i - s_pfx[j];
+          const uint32_t r = rel / nvec, ch = rel - r * nvec;
+          const int l = s_order[j];
+          goff = vrow0 + ((uint32_t)s_lvl[l].start + r) * rs + ch * VB;
+          dst[k] = ((uint32_t)s_loff[l] + r) * lrs + ch * VB;
+        }
+        v[k] = buf_load<VB>(rv, goff);
+      }
+#pragma unroll
+      for (int k = 0; k < KB; ++k)
+        if (dst[k] != 0xffffffffu) *reinterpret_cast<RawVec<VB>*>(s_rows + dst[k]) = v[k];
+    }
+  }
+  __syncthreads();
+
+  const uint32_t lanes_log2 = (uint32_t)p.lpu_log2;
+  const uint32_t lane = threadIdx.x & ((1u << lanes_log2) - 1u);
+  const uint32_t upi = (uint32_t)NT >> lanes_log2;  // units per iteration
+  if ((int)lane >= p.nvec) return;  // no barrier follows
+  for (uint32_t qb = q0; qb < q1; qb += upi) {
+    const uint32_t q = qb + (threadIdx.x >> lanes_log2);
+    if (q >= q1) break;
+    const uint32_t bqh = (b * p.Q + q) * (uint32_t)p.H + h;
+    float acc[VEC];
+    unit_forward<DIM, EV, EC, VEC, PT, true>(p, s_lvl, s_loff, s_rows, b, h, bqh, lane, acc);
+    typename EV::T* outp = static_cast<typename EV::T*>(p.out) + (size_t)bqh * p.C + lane * VEC;
+    store_vec<EV, VEC>(outp, acc);
+  }
+}
+
+// The compile-time point counts (4 and 8 points per level) need aligned coordinate blocks
+// and a unit's blocks within kFwdCoordSlots per lane.
+template <int DIM, int PT>
+static bool pt_path(const Params& p) {
+  constexpr int SB = DIM == 2 ? (PT < 4 ? PT : 4) : (PT < 2 ? PT : 2);
+  return p.P == PT && p.coords_aligned && p.L * (PT / SB) <= kFwdCoordSlots<DIM> * p.nvec;
+}
+
 template <int DIM, typename EV, typename EC, int VEC>
 static hipError_t launch_fwd(const Params& p, hipStream_t s) {
-  // compile-time point counts for the common 4 and 8 points per level
-  if (p.P == 4 && p.coords_aligned)
+  if (pt_path<DIM, 4>(p))
     hipLaunchKernelGGL((msda_fwd_kernel<DIM, EV, EC, VEC, 4>), dim3(p.nblocks), dim3(kBlock), 0, s, p);
-  else if (p.P == 8 && p.coords_aligned)
+  else if (pt_path<DIM, 8>(p))
     hipLaunchKernelGGL((msda_fwd_kernel<DIM, EV, EC, VEC, 8>), dim3(p.nblocks), dim3(kBlock), 0, s, p);
   else
     hipLaunchKernelGGL((msda_fwd_kernel<DIM, EV, EC, VEC, 0>), dim3(p.nblocks), dim3(kBlock), 0, s, p);
   return hipGetLastError();
 }
 
+template <int DIM, typename EV, typename EC, int VEC>
+static hipError_t launch_fwd_staged(const Params& p, hipStream_t s) {
+  const dim3 g(p.nblocks), t(kFwdStageThreads);
+  if (pt_path<DIM, 4>(p))
+    hipLaunchKernelGGL((msda_fwd_staged_kernel<DIM, EV, EC, VEC, 4>), g, t, p.stage_bytes, s, p);
+  else if (pt_path<DIM, 8>(p))
+    hipLaunchKernelGGL((msda_fwd_staged_kernel<DIM, EV, EC, VEC, 8>), g, t, p.stage_bytes, s, p);
+  else
+    hipLaunchKernelGGL((msda_fwd_staged_kernel<DIM, EV, EC, VEC, 0>), g, t, p.stage_bytes, s, p);
+  return hipGetLastError();
+}
+
 template <int DIM, typename EV, typename EC>
-static LaunchFn pick_vec(int vec_bytes) {
+static LaunchFn pick_vec(int vec_bytes, bool staged) {
   constexpr int S = EV::kBytes;
   switch (vec_bytes) {
-    case 16: return &launch_fwd<DIM, EV, EC, 16 / S>;
-    case 8: return &launch_fwd<DIM, EV, EC, 8 / S>;
-    case 4: return &launch_fwd<DIM, EV, EC, 4 / S>;
+    case 16: return staged ? &launch_fwd_staged<DIM, EV, EC, 16 / S> : &launch_fwd<DIM, EV, EC, 16 / S>;
+    case 8: return staged ? &launch_fwd_staged<DIM, EV, EC, 8 / S> : &launch_fwd<DIM, EV, EC, 8 / S>;
+    case 4: return staged ? &launch_fwd_staged<DIM, EV, EC, 4 / S> : &launch_fwd<DIM, EV, EC, 4 / S>;
     case 2:
-      if constexpr (S == 2) return &launch_fwd<DIM, EV, EC, 1>;
+      if constexpr (S == 2) return staged ? &launch_fwd_staged<DIM, EV, EC, 1> : &launch_fwd<DIM, EV, EC, 1>;
       return nullptr;
     default: return nullptr;
   }
 }
 
 template <int DIM>
-static LaunchFn pick_types(int vdt, int cdt, int vec_bytes) {
-  if (vdt == 0 && cdt == 0) return pick_vec<DIM, F32, F32>(vec_bytes);
-  if (vdt == 1 && cdt == 1) return pick_vec<DIM, F16, F16>(vec_bytes);
-  if (vdt == 1 && cdt == 0) return pick_vec<DIM, F16, F32>(vec_bytes);
-  if (vdt == 2 && cdt == 2) return pick_vec<DIM, BF16, BF16>(vec_bytes);
-  if (vdt == 2 && cdt == 0) return pick_vec<DIM, BF16, F32>(vec_bytes);
+static LaunchFn pick_types(int vdt, int cdt, int vec_bytes, bool staged) {
+  if (vdt == 0 && cdt == 0) return pick_vec<DIM, F32, F32>(vec_bytes, staged);
+  if (vdt == 1 && cdt == 1) return pick_vec<DIM, F16, F16>(vec_bytes, staged);
+  if (vdt == 1 && cdt == 0) return pick_vec<DIM, F16, F32>(vec_bytes, staged);
+  if (vdt == 2 && cdt == 2) return pick_vec<DIM, BF16, BF16>(vec_bytes, staged);
+  if (vdt == 2 && cdt == 0) return pick_vec<DIM, BF16, F32>(vec_bytes, staged);
   return nullptr;
 }
 
-LaunchFn get_fwd_launcher(int dim, int vdt, int cdt, int vec_bytes) {
-  if (dim == 2) return pick_types<2>(vdt, cdt, vec_bytes);
-  if (dim == 3) return pick_types<3>(vdt, cdt, vec_bytes);
+LaunchFn get_fwd_launcher(int dim, int vdt, int cdt, int vec_bytes, bool staged) {
+  if (dim == 2) return pick_types<2>(vdt, cdt, vec_bytes, staged);
+  if (dim == 3) return pick_types<3>(vdt, cdt, vec_bytes, staged);
   return nullptr;
 }
 

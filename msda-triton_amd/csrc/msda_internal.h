@@ -17,6 +17,12 @@ constexpr int kTileWavesPerSimd = 4;  // tile-kernel occupancy target: two workg
 constexpr int kFillStage = 2048;      // records staged in LDS per fill round
 constexpr int kGradThreads = 256;     // threads of the backward sample-gradient kernel
 constexpr int kGradRounds = 4;        // unit groups each of its threads handles in turn
+constexpr int kFwdStageThreads = 1024;            // threads of the staged forward kernel
+constexpr uint32_t kFwdStageLds = 156 * 1024;     // its dynamic LDS: one workgroup per CU
+constexpr uint32_t kFwdStageMinQueries = 512;     // queries per workgroup that pay for staging
+// coordinate blocks a forward lane holds (2D: 4-sample blocks, 3D: 2-sample blocks)
+template <int DIM>
+constexpr int kFwdCoordSlots = DIM == 2 ? 2 : 4;
 
 // Forward parameters for one launch over a contiguous range of batches. Pointers are
 // already offset to the first batch of the range; all in-kernel offsets are 32-bit.
@@ -40,12 +46,18 @@ struct Params {
   float lo_g, hi_g;        // grid clamp bounds as fp32
   uint32_t nblocks;
   int32_t coords_aligned;  // loc and attn are 16-byte aligned: per-level block loads allowed
+  // staged path: one workgroup per (batch, head, query range) keeps the smallest levels of
+  // its (batch, head) value slice in LDS
+  uint32_t splits;         // workgroups per (batch, head)
+  uint32_t qper;           // queries per workgroup
+  uint32_t stage_bytes;    // LDS bytes for staged rows
 };
 
 using LaunchFn = hipError_t (*)(const Params&, hipStream_t);
 
 // Forward launcher for (dim, value dtype, coord dtype, bytes per lane load), or nullptr.
-LaunchFn get_fwd_launcher(int dim, int vdt, int cdt, int vec_bytes);
+// `staged` selects the kernel that serves small levels from LDS (Params.splits/qper set).
+LaunchFn get_fwd_launcher(int dim, int vdt, int cdt, int vec_bytes, bool staged);
 
 // ---------------------------------------------------------------------------------------
 // Backward. grad_value is accumulated in key order. Every sample with a valid corner is
