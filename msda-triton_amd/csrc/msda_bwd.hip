@@ -161,22 +161,29 @@ __device__ inline bool sample_tile(const BwdPlan& pl, const BwdLevel& lv, const 
 // d/d(attn) and (clamp-masked) d/d(loc) summed over the unit's lanes, so every lane of
 // the group holds them. out = {grad_attn, grad_loc x, y[, z]}.
 template <int DIM, typename EV, int VEC, int NC = (1 << DIM)>
-__device__ inline void sample_grads(const BwdPlan& pl, const BwdLevel& lv, const Sample<DIM>& sm,
-                                    const RawVec<VEC * EV::kBytes> (&raw)[NC], const float (&gr)[VEC],
-                                    float a, float (&out)[DIM + 1]) {
+__device__ inline void sample_grads(const BwdLevel& lv, const Sample<DIM>& sm,
+                                    const RawVec<VEC * EV::kBytes> (&raw)[NC],
+                                    const RawVec<VEC * EV::kBytes>& graw, float a, int lg,
+                                    float (&out)[DIM + 1]) {
   float dot[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
-    float v[VEC];
-    widen<EV, VEC>(raw[c], v);
     float d = 0.0f;
+    if constexpr (EV::kBytes == 2 && VEC >= 2) {
+      // value and grad_out are both 16-bit: packed dot products, exact products
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) d = __builtin_fmaf(gr[e], v[e], d);
+      for (int e = 0; e < VEC / 2; ++e) d = dot2_acc<EV>(raw_dword(raw[c], e), raw_dword(graw, e), d);
+    } else {
+      float v[VEC], g[VEC];
+      widen<EV, VEC>(raw[c], v);
+      widen<EV, VEC>(graw, g);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) d = __builtin_fmaf(g[e], v[e], d);
+    }
     dot[c] = d;
   }
   float s_attn, s_x, s_y, s_z;
   corner_grads<DIM>(sm, dot, s_attn, s_x, s_y, s_z);
-  const int lg = pl.lpu_log2;
   out[0] = group_sum(s_attn, lg);
   s_x = group_sum(s_x, lg);
   s_y = group_sum(s_y, lg);
@@ -229,7 +236,8 @@ __device__ inline bool sample_rows(const BwdPlan& pl, const BwdLevel& lv, const 
 // corner get zero gradients. PT > 0: P is a compile-time constant; each batch's
 // coordinates and weights are one block load per lane, queued behind the previous
 // batch's corner rows, and all SB*2^DIM corner rows of a batch are in flight together.
-template <int DIM, typename EV, typename EC, int VEC, int PT>
+// LG >= 0: lanes per unit (2^LG) is a compile-time constant, else pl.lpu_log2.
+template <int DIM, typename EV, typename EC, int VEC, int PT, int LG>
 __global__ __launch_bounds__(kGradThreads) void bwd_grad_kernel(const BwdPlan pl, const BwdBuffers bf) {
   constexpr int VB = VEC * EV::kBytes;
   constexpr int NC = 1 << DIM;
@@ -244,7 +252,7 @@ __global__ __launch_bounds__(kGradThreads) void bwd_grad_kernel(const BwdPlan pl
   for (int i = threadIdx.x; i < pl.bins; i += kGradThreads) s_hist[i] = 0;
   __syncthreads();
 
-  const int lg = pl.lpu_log2;
+  const int lg = LG >= 0 ? LG : pl.lpu_log2;
   const uint32_t lanes = 1u << lg;
   const uint32_t lane = threadIdx.x & (lanes - 1u);
   const bool act = (int)lane < pl.nvec;
@@ -256,13 +264,8 @@ __global__ __launch_bounds__(kGradThreads) void bwd_grad_kernel(const BwdPlan pl
 #pragma unroll 1
   for (uint32_t wi = threadIdx.x >> lg; wi < units; wi += gpw) {
     const BinUnit bu = bin_unit(pl, g, w, wi);
-    float gr[VEC];
-    if (act) {
-      widen<EV, VEC>(glb_load<VB>(static_cast<const TV*>(bf.grad_out) + bu.bqh * pl.C + lane * VEC), gr);
-    } else {
-#pragma unroll
-      for (int k = 0; k < VEC; ++k) gr[k] = 0.0f;
-    }
+    RawVec<VB> gr = {};
+    if (act) gr = glb_load<VB>(static_cast<const TV*>(bf.grad_out) + bu.bqh * pl.C + lane * VEC);
     const uint32_t vbase =
         ((bu.b * (uint32_t)pl.K * (uint32_t)pl.H + bu.h) * (uint32_t)pl.C + (act ? lane : 0u) * VEC) *
         EV::kBytes;
@@ -308,7 +311,7 @@ __global__ __launch_bounds__(kGradThreads) void bwd_grad_kernel(const BwdPlan pl
 #pragma unroll
         for (int k = 0; k < SB; ++k) {
           float o[DIM + 1];
-          sample_grads<DIM, EV, VEC>(pl, lv, sm[k], raw[k], gr, a[k], o);
+          sample_grads<DIM, EV, VEC>(lv, sm[k], raw[k], gr, a[k], lg, o);
           ga[k] = o[0];
 #pragma unroll
           for (int d = 0; d < DIM; ++d) gl[k * DIM + d] = o[1 + d];
@@ -346,7 +349,7 @@ __global__ __launch_bounds__(kGradThreads) void bwd_grad_kernel(const BwdPlan pl
             if (p0 + k >= pl.P) continue;
             const int s = l * pl.P + p0 + k;
             float o[DIM + 1];
-            sample_grads<DIM, EV, VEC>(pl, lv, sm[k], raw[k], gr, (float)attp[s], o);
+            sample_grads<DIM, EV, VEC>(lv, sm[k], raw[k], gr, (float)attp[s], lg, o);
             if (lane == ((uint32_t)k & (lanes - 1u))) {
               gap[s] = (TC)o[0];
 #pragma unroll
@@ -764,14 +767,27 @@ hipError_t run_bwd_t(const BwdPlan& pl, const BwdBuffers& bf, hipStream_t s) {
   const uint32_t nbin_wg = (uint32_t)pl.groups * (uint32_t)pl.wgpg;
   const size_t hist_bytes = (size_t)pl.bins * sizeof(uint32_t);
   if (nbin_wg == 0) return hipErrorInvalidValue;
-  if (pl.P == 4 && pl.coords_aligned)
-    hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 4>), dim3(nbin_wg), dim3(kGradThreads),
+  // compile-time lane-group size for the common 16-byte lane loads of 4 or 8 lanes per unit
+  if (pl.P == 4 && pl.coords_aligned && pl.lpu_log2 == 2)
+    hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 4, 2>), dim3(nbin_wg), dim3(kGradThreads),
+                       hist_bytes, s, pl, bf);
+  else if (pl.P == 4 && pl.coords_aligned && pl.lpu_log2 == 3)
+    hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 4, 3>), dim3(nbin_wg), dim3(kGradThreads),
+                       hist_bytes, s, pl, bf);
+  else if (pl.P == 8 && pl.coords_aligned && pl.lpu_log2 == 2)
+    hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 8, 2>), dim3(nbin_wg), dim3(kGradThreads),
+                       hist_bytes, s, pl, bf);
+  else if (pl.P == 8 && pl.coords_aligned && pl.lpu_log2 == 3)
+    hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 8, 3>), dim3(nbin_wg), dim3(kGradThreads),
+                       hist_bytes, s, pl, bf);
+  else if (pl.P == 4 && pl.coords_aligned)
+    hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 4, -1>), dim3(nbin_wg), dim3(kGradThreads),
                        hist_bytes, s, pl, bf);
   else if (pl.P == 8 && pl.coords_aligned)
-    hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 8>), dim3(nbin_wg), dim3(kGradThreads),
+    hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 8, -1>), dim3(nbin_wg), dim3(kGradThreads),
                        hist_bytes, s, pl, bf);
   else
-    hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 0>), dim3(nbin_wg), dim3(kGradThreads),
+    hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 0, -1>), dim3(nbin_wg), dim3(kGradThreads),
                        hist_bytes, s, pl, bf);
   if (pl.T == 0) return hipGetLastError();  // no cell in any level: grad_value is empty
   const uint32_t waves_per_block = kBlock / kWave;

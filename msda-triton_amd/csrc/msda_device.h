@@ -156,6 +156,21 @@ __device__ inline void widen(const RawVec<VEC * E::kBytes>& r, float (&o)[VEC]) 
   }
 }
 
+// acc + a.lo * b.lo + a.hi * b.hi for two packed 16-bit pairs, in fp32. Both products of
+// 16-bit floats are exact in fp32, so this equals two fp32 FMAs on the widened values up
+// to the rounding of the sum.
+template <typename E>
+__device__ inline float dot2_acc(uint32_t a, uint32_t b, float acc) {
+  if constexpr (__is_same(E, BF16)) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a), __builtin_bit_cast(bf2, b), acc,
+                                           false);
+  } else {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b), acc, false);
+  }
+}
+
 // fp32 -> storage type, round to nearest even (hardware conversions on gfx950).
 template <typename E>
 __device__ inline typename E::T narrow(float x) {
