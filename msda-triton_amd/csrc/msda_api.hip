@@ -415,7 +415,9 @@ int msda_fwd(const msda_desc* d, const void* value, const int32_t* spatial_shape
     const uint64_t slices = (uint64_t)bc * d->num_heads;
     const uint64_t splits = (kCus + slices - 1) / slices;
     const uint64_t qper = ((uint64_t)d->num_queries + splits - 1) / splits;
-    const bool staged = has_samples && qper >= msda::kFwdStageMinQueries;
+    // the LDS holds at least one staged row beside the all-zero row
+    const bool staged = has_samples && qper >= msda::kFwdStageMinQueries &&
+                        (uint64_t)d->channels * sv * 2 <= msda::kFwdStageLds;
     if (staged) {
       p.splits = (uint32_t)splits;
       p.qper = (uint32_t)qper;

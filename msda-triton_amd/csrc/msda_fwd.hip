@@ -47,10 +47,36 @@ __device__ inline bool decode_unit(const Params& p, Unit& u) {
   return true;
 }
 
+// Per-level addressing of the forward. A corner row (x, y, z) of a level is read at byte
+// offset  unit base + base + z*sz + y*sy + x*sx  from the value slice (global levels, unit
+// base = the unit's (b, h, lane) offset) or from the staged rows in LDS (unit base = the
+// lane's offset in a row).
+struct FwdLevel {
+  int32_t start, W, H, D;  // first row in K and extents (D = 1 in 2D)
+  uint32_t base;           // global: start * rs; staged: first LDS byte of the level
+  int32_t sx, sy, sz;      // byte strides along x, y, z
+  int32_t flags;           // kLvlStaged | kLvlMul24
+};
+constexpr int32_t kLvlStaged = 1;  // rows are in LDS
+constexpr int32_t kLvlMul24 = 2;   // strides and extents fit 24-bit signed multiplies
+
+// Strides of a level whose rows are sx bytes apart; kLvlMul24 when every product of an
+// index in [-2, extent + 1] and a stride fits the 24-bit multiplier.
+__device__ inline void set_strides(FwdLevel& e, uint32_t sx) {
+  const uint64_t sy = (uint64_t)e.W * sx, sz = sy * (uint64_t)e.H;
+  constexpr uint64_t lim = 1u << 23;
+  e.sx = (int32_t)sx;
+  e.sy = (int32_t)sy;
+  e.sz = (int32_t)sz;
+  const bool m24 = sx < lim && sy < lim && sz < lim && (uint64_t)e.D + 2 < lim;
+  e.flags = (e.flags & ~kLvlMul24) | (m24 ? kLvlMul24 : 0);
+}
+
+// Level table for global reads with rows rs bytes apart.
 template <int DIM>
-__device__ inline void stage_levels(const Params& p, Level* s_lvl) {
+__device__ inline void stage_levels(const Params& p, FwdLevel* s_lvl, uint32_t rs) {
   for (int i = threadIdx.x; i < p.L; i += blockDim.x) {
-    Level e;
+    FwdLevel e;
     e.start = p.starts[i];
     if constexpr (DIM == 2) {
       e.D = 1;
@@ -61,46 +87,58 @@ __device__ inline void stage_levels(const Params& p, Level* s_lvl) {
       e.H = p.shapes[3 * i + 1];
       e.W = p.shapes[3 * i + 2];
     }
+    e.base = (uint32_t)e.start * rs;
+    e.flags = 0;
+    set_strides(e, rs);
     s_lvl[i] = e;
   }
 }
 
 // Corner rows of a batch of samples: from the global value slice through the buffer range
-// check (zero outside the level), or, for a level held in LDS, from its staged rows (zero
-// outside the level by selection).
-template <int DIM, int VB, int SB, bool LDS>
-__device__ inline void fetch_rows(const Sample<DIM> (&sm)[SB], const Level& lv,
-                                  __amdgpu_buffer_rsrc_t rv, uint32_t vbase, uint32_t rs,
-                                  const char* s_rows, int32_t lrow, uint32_t lane_off,
-                                  RawVec<VB> (&raw)[SB][1 << DIM]) {
+// check (kOobOffset reads zero), or, for a level held in LDS, from its staged rows (invalid
+// corners read the all-zero row at zoff). ubase is the unit's byte base (see FwdLevel).
+// M24: the level's strides fit 24-bit multiplies (full-rate v_mad_i32_i24 instead of
+// quarter-rate 32-bit multiplies).
+template <int DIM, int VB, int SB, bool LDS, bool M24>
+__device__ inline void fetch_rows(const Sample<DIM> (&sm)[SB], const FwdLevel& lv,
+                                  __amdgpu_buffer_rsrc_t rv, uint32_t ubase, const char* s_rows,
+                                  uint32_t zoff, RawVec<VB> (&raw)[SB][1 << DIM]) {
   constexpr int NC = 1 << DIM;
-  const uint32_t W = (uint32_t)lv.W, HW = (uint32_t)lv.W * (uint32_t)lv.H;
 #pragma unroll
   for (int k = 0; k < SB; ++k) {
-    uint32_t row0 = (uint32_t)sm[k].ay.i0 * W + (uint32_t)sm[k].ax.i0;
-    if constexpr (DIM == 3) row0 += (uint32_t)sm[k].az.i0 * HW;
+    int32_t o0;
+    if constexpr (M24) {
+      o0 = __mul24(sm[k].ay.i0, lv.sy) + __mul24(sm[k].ax.i0, lv.sx);
+      if constexpr (DIM == 3) o0 += __mul24(sm[k].az.i0, lv.sz);
+    } else {
+      o0 = sm[k].ay.i0 * lv.sy + sm[k].ax.i0 * lv.sx;
+      if constexpr (DIM == 3) o0 += sm[k].az.i0 * lv.sz;
+    }
+    const uint32_t o = ubase + lv.base + (uint32_t)o0;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const uint32_t dr = ((c & 1) ? 1u : 0u) + ((c & 2) ? W : 0u) + ((DIM == 3 && (c & 4)) ? HW : 0u);
+      const uint32_t dr = ((c & 1) ? (uint32_t)lv.sx : 0u) + ((c & 2) ? (uint32_t)lv.sy : 0u) +
+                          ((DIM == 3 && (c & 4)) ? (uint32_t)lv.sz : 0u);
       const bool ok = corner_valid<DIM>(c, sm[k]);
-      if constexpr (LDS) {
-        // row stride of the staged slice is rs (= C * element size) as well
-        const uint32_t off = ok ? ((uint32_t)lrow + row0 + dr) * rs + lane_off : lane_off;
-        RawVec<VB> v = *reinterpret_cast<const RawVec<VB>*>(s_rows + off);
-        if constexpr (VB >= 4) {
-#pragma unroll
-          for (int i = 0; i < VB / 4; ++i) {
-            if constexpr (VB == 4) v.v = ok ? v.v : 0u;
-            else v.v[i] = ok ? v.v[i] : 0u;
-          }
-        } else {
-          v.v = ok ? v.v : (uint16_t)0;
-        }
-        raw[k][c] = v;
-      } else {
-        raw[k][c] = buf_load<VB>(rv, ok ? vbase + ((uint32_t)lv.start + row0 + dr) * rs : kOobOffset);
-      }
+      if constexpr (LDS)
+        raw[k][c] = *reinterpret_cast<const RawVec<VB>*>(s_rows + (ok ? o + dr : zoff));
+      else
+        raw[k][c] = buf_load<VB>(rv, ok ? o + dr : kOobOffset);
     }
+  }
+}
+
+// fetch_rows with the level's storage and multiplier chosen at run time (uniform branch).
+template <int DIM, int VB, int SB, bool STAGED>
+__device__ inline void fetch_level(const Sample<DIM> (&sm)[SB], const FwdLevel& lv,
+                                   __amdgpu_buffer_rsrc_t rv, uint32_t vbase, uint32_t lane_off,
+                                   const char* s_rows, uint32_t zoff, RawVec<VB> (&raw)[SB][1 << DIM]) {
+  if (STAGED && (lv.flags & kLvlStaged)) {
+    if (lv.flags & kLvlMul24) fetch_rows<DIM, VB, SB, true, true>(sm, lv, rv, lane_off, s_rows, zoff, raw);
+    else fetch_rows<DIM, VB, SB, true, false>(sm, lv, rv, lane_off, s_rows, zoff, raw);
+  } else {
+    if (lv.flags & kLvlMul24) fetch_rows<DIM, VB, SB, false, true>(sm, lv, rv, vbase, s_rows, zoff, raw);
+    else fetch_rows<DIM, VB, SB, false, false>(sm, lv, rv, vbase, s_rows, zoff, raw);
   }
 }
 
@@ -112,10 +150,11 @@ __device__ inline void fetch_rows(const Sample<DIM> (&sm)[SB], const Level& lv,
 // per lane (L * P / SB <= kFwdCoordSlots * nvec). PT == 0 handles any P with per-sample
 // loads.
 //
-// STAGED: s_loff[l] >= 0 gives the first LDS row of level l in s_rows (rows of rs bytes).
+// STAGED: levels flagged kLvlStaged are read from s_rows; zoff is the lane's offset in the
+// all-zero row there.
 template <int DIM, typename EV, typename EC, int VEC, int PT, bool STAGED>
-__device__ inline void unit_forward(const Params& p, const Level* s_lvl, const int32_t* s_loff,
-                                    const char* s_rows, uint32_t b, uint32_t h, uint32_t bqh,
+__device__ inline void unit_forward(const Params& p, const FwdLevel* s_lvl, const char* s_rows,
+                                    uint32_t zoff, uint32_t b, uint32_t h, uint32_t bqh,
                                     uint32_t lane, float (&acc)[VEC]) {
   constexpr int VB = VEC * EV::kBytes;
   constexpr int NC = 1 << DIM;
@@ -125,10 +164,8 @@ __device__ inline void unit_forward(const Params& p, const Level* s_lvl, const i
   const TC* locp = static_cast<const TC*>(p.loc) + (size_t)bqh * (LP * DIM);
   const TC* attp = static_cast<const TC*>(p.attn) + (size_t)bqh * LP;
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.value, p.value_bytes);
-  const uint32_t rs = (uint32_t)p.H * (uint32_t)p.C * EV::kBytes;  // bytes between rows of K
   const uint32_t lane_off = lane * VB;
   const uint32_t vbase = ((b * (uint32_t)p.K * (uint32_t)p.H + h) * (uint32_t)p.C) * EV::kBytes + lane_off;
-  const uint32_t lrs = (uint32_t)p.C * EV::kBytes;  // bytes per staged row
 
 #pragma unroll
   for (int i = 0; i < VEC; ++i) acc[i] = 0.0f;
@@ -156,7 +193,7 @@ __device__ inline void unit_forward(const Params& p, const Level* s_lvl, const i
 #pragma unroll 1
     for (int bi = 0; bi < nbatch; ++bi) {
       const int l = bi / BPL;
-      const Level lv = s_lvl[l];
+      const FwdLevel lv = s_lvl[l];
       const int sl = bi / nv;
       const int src = (gbase + (bi - sl * nv)) << 2;
       CoordBlock<EC, SB * DIM> lb;
@@ -188,11 +225,7 @@ __device__ inline void unit_forward(const Params& p, const Level* s_lvl, const i
         for (int c = 0; c < NC; ++c) cw[k][c] = corner_weight<DIM>(c, sm[k]) * a;
       }
       RawVec<VB> raw[SB][NC];
-      const int32_t lrow = STAGED ? s_loff[l] : -1;
-      if (STAGED && lrow >= 0)
-        fetch_rows<DIM, VB, SB, true>(sm, lv, rv, vbase, lrs, s_rows, lrow, lane_off, raw);
-      else
-        fetch_rows<DIM, VB, SB, false>(sm, lv, rv, vbase, rs, s_rows, lrow, lane_off, raw);
+      fetch_level<DIM, VB, SB, STAGED>(sm, lv, rv, vbase, lane_off, s_rows, zoff, raw);
 #pragma unroll
       for (int k = 0; k < SB; ++k) {
 #pragma unroll
@@ -206,8 +239,7 @@ __device__ inline void unit_forward(const Params& p, const Level* s_lvl, const i
     }
   } else {
     for (int l = 0; l < p.L; ++l) {
-      const Level lv = s_lvl[l];
-      const int32_t lrow = STAGED ? s_loff[l] : -1;
+      const FwdLevel lv = s_lvl[l];
       for (int p0 = 0; p0 < p.P; p0 += SB) {
         Sample<DIM> sm[SB];
         float cw[SB][NC];
@@ -216,15 +248,15 @@ __device__ inline void unit_forward(const Params& p, const Level* s_lvl, const i
           const int s = l * p.P + p0 + k;
           const bool live = p0 + k < p.P;
           const float a = live ? (float)attp[s] : 0.0f;
-          sm[k] = make_sample<DIM>(locp + (live ? s : 0) * DIM, lv, p.clamp, p.lo_g, p.hi_g);
+          const TC* lp = locp + (live ? s : 0) * DIM;
+          sm[k].ax = make_axis((float)lp[0], (float)lv.W, lv.W, p.clamp, p.lo_g, p.hi_g);
+          sm[k].ay = make_axis((float)lp[1], (float)lv.H, lv.H, p.clamp, p.lo_g, p.hi_g);
+          if constexpr (DIM == 3) sm[k].az = make_axis((float)lp[2], (float)lv.D, lv.D, p.clamp, p.lo_g, p.hi_g);
 #pragma unroll
           for (int c = 0; c < NC; ++c) cw[k][c] = corner_weight<DIM>(c, sm[k]) * a;
         }
         RawVec<VB> raw[SB][NC];
-        if (STAGED && lrow >= 0)
-          fetch_rows<DIM, VB, SB, true>(sm, lv, rv, vbase, lrs, s_rows, lrow, lane_off, raw);
-        else
-          fetch_rows<DIM, VB, SB, false>(sm, lv, rv, vbase, rs, s_rows, lrow, lane_off, raw);
+        fetch_level<DIM, VB, SB, STAGED>(sm, lv, rv, vbase, lane_off, s_rows, zoff, raw);
 #pragma unroll
         for (int k = 0; k < SB; ++k) {
 #pragma unroll
@@ -250,14 +282,14 @@ __device__ inline void unit_forward(const Params& p, const Level* s_lvl, const i
 // dtype directly instead of an fp32 (B*H, Q, C) scratch plus permute (msda_2d.py:649-651).
 template <int DIM, typename EV, typename EC, int VEC, int PT>
 __global__ __launch_bounds__(kBlock) void msda_fwd_kernel(const Params p) {
-  __shared__ Level s_lvl[kMaxLevels];
-  stage_levels<DIM>(p, s_lvl);
+  __shared__ FwdLevel s_lvl[kMaxLevels];
+  stage_levels<DIM>(p, s_lvl, (uint32_t)p.H * (uint32_t)p.C * EV::kBytes);
   __syncthreads();
   Unit u;
   if (!decode_unit(p, u)) return;
   if ((int)u.lane >= p.nvec) return;
   float acc[VEC];
-  unit_forward<DIM, EV, EC, VEC, PT, false>(p, s_lvl, nullptr, nullptr, u.b, u.h, u.bqh, u.lane, acc);
+  unit_forward<DIM, EV, EC, VEC, PT, false>(p, s_lvl, nullptr, 0u, u.b, u.h, u.bqh, u.lane, acc);
   typename EV::T* outp = static_cast<typename EV::T*>(p.out) + (size_t)u.bqh * p.C + u.lane * VEC;
   store_vec<EV, VEC>(outp, acc);
 }
@@ -269,26 +301,24 @@ __global__ __launch_bounds__(kFwdStageThreads) void msda_fwd_staged_kernel(const
   constexpr int NT = kFwdStageThreads;
   constexpr int VB = VEC * EV::kBytes;
   extern __shared__ __attribute__((aligned(16))) char s_rows[];
-  __shared__ Level s_lvl[kMaxLevels];
-  __shared__ int32_t s_loff[kMaxLevels];  // first LDS row of a staged level, else -1
+  __shared__ FwdLevel s_lvl[kMaxLevels];
   __shared__ int32_t s_order[kMaxLevels];  // staged levels in LDS order
   __shared__ uint32_t s_pfx[kMaxLevels + 1];  // their first piece in the flat staging index
   __shared__ int32_t s_nst;
-  stage_levels<DIM>(p, s_lvl);
-  __syncthreads();
   const uint32_t lrs = (uint32_t)p.C * EV::kBytes;  // bytes per staged row
+  stage_levels<DIM>(p, s_lvl, (uint32_t)p.H * (uint32_t)p.C * EV::kBytes);
+  __syncthreads();
   const uint32_t nvec = (uint32_t)p.nvec;
   if (threadIdx.x == 0) {
-    // greedy: smallest levels first, while they fit
-    const uint32_t cap = p.stage_bytes / lrs;
+    // greedy: smallest levels first, while they fit beside the all-zero row
+    const uint32_t cap = p.stage_bytes / lrs - 1u;  // the host guarantees >= 2 rows
     uint32_t used = 0;
     int n = 0;
-    for (int l = 0; l < p.L; ++l) s_loff[l] = -1;
     for (;;) {
       int best = -1;
       uint32_t bsz = 0;
       for (int l = 0; l < p.L; ++l) {
-        if (s_loff[l] >= 0) continue;
+        if (s_lvl[l].flags & kLvlStaged) continue;
         const uint32_t sz = (uint32_t)s_lvl[l].W * (uint32_t)s_lvl[l].H * (uint32_t)s_lvl[l].D;
         if (sz == 0 || used + sz > cap) continue;
         if (best < 0 || sz < bsz) {
@@ -297,7 +327,10 @@ __global__ __launch_bounds__(kFwdStageThreads) void msda_fwd_staged_kernel(const
         }
       }
       if (best < 0) break;
-      s_loff[best] = (int32_t)used;
+      FwdLevel& e = s_lvl[best];
+      e.flags |= kLvlStaged;
+      e.base = used * lrs;
+      set_strides(e, lrs);
       s_order[n] = best;
       s_pfx[n] = used * nvec;
       used += bsz;
@@ -307,6 +340,7 @@ __global__ __launch_bounds__(kFwdStageThreads) void msda_fwd_staged_kernel(const
     s_nst = n;
   }
   __syncthreads();
+  const uint32_t zrow = s_pfx[s_nst] / nvec * lrs;  // byte offset of the all-zero row
 
   const uint32_t lb = xcd_logical_block(blockIdx.x, p.nblocks);
   const uint32_t bh = lb / p.splits, split = lb - bh * p.splits;
@@ -338,7 +372,7 @@ __global__ __launch_bounds__(kFwdStageThreads) void msda_fwd_staged_kernel(const
           const uint32_t r = rel / nvec, ch = rel - r * nvec;
           const int l = s_order[j];
           goff = vrow0 + ((uint32_t)s_lvl[l].start + r) * rs + ch * VB;
-          dst[k] = ((uint32_t)s_loff[l] + r) * lrs + ch * VB;
+          dst[k] = s_lvl[l].base + r * lrs + ch * VB;
         }
         v[k] = buf_load<VB>(rv, goff);
       }
@@ -346,6 +380,7 @@ __global__ __launch_bounds__(kFwdStageThreads) void msda_fwd_staged_kernel(const
       for (int k = 0; k < KB; ++k)
         if (dst[k] != 0xffffffffu) *reinterpret_cast<RawVec<VB>*>(s_rows + dst[k]) = v[k];
     }
+    if (threadIdx.x < nvec) *reinterpret_cast<RawVec<VB>*>(s_rows + zrow + threadIdx.x * VB) = RawVec<VB>{};
   }
   __syncthreads();
 
@@ -358,7 +393,7 @@ __global__ __launch_bounds__(kFwdStageThreads) void msda_fwd_staged_kernel(const
     if (q >= q1) break;
     const uint32_t bqh = (b * p.Q + q) * (uint32_t)p.H + h;
     float acc[VEC];
-    unit_forward<DIM, EV, EC, VEC, PT, true>(p, s_lvl, s_loff, s_rows, b, h, bqh, lane, acc);
+    unit_forward<DIM, EV, EC, VEC, PT, true>(p, s_lvl, s_rows, zrow + lane * VB, b, h, bqh, lane, acc);
     typename EV::T* outp = static_cast<typename EV::T*>(p.out) + (size_t)bqh * p.C + lane * VEC;
     store_vec<EV, VEC>(outp, acc);
   }
