@@ -288,8 +288,20 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
   pl.lds_bytes = lds;
   // tiles of the coarsest level first: its chunks are the longest, so they start early
   int tiles = 0;
+  bool mul24 = (uint64_t)d->num_heads * d->channels * s < (1u << 23);
   for (int l = d->num_levels - 1; l >= 0; --l) {
     msda::BwdLevel& lv = pl.lv[l];
+    const uint64_t rsb = (uint64_t)d->num_heads * d->channels * s;  // bytes between rows of K
+    lv.base = (uint32_t)((uint64_t)lv.start * rsb);
+    lv.sy = (int32_t)((uint64_t)lv.W * rsb);
+    lv.sz = (int32_t)((uint64_t)lv.W * lv.H * rsb);
+    {
+      // largest stride used (y in 2D, z in 3D) and largest corner index must fit 24 bits
+      const uint64_t lim = 1u << 23;
+      const uint64_t top = (uint64_t)lv.W * (d->dim == 3 ? (uint64_t)lv.H : 1u) * rsb;
+      const int64_t ext = (lv.W > lv.H ? (lv.W > lv.D ? lv.W : lv.D) : (lv.H > lv.D ? lv.H : lv.D)) + 2;
+      if (top >= lim || (uint64_t)ext >= lim) mul24 = false;
+    }
     lv.ntx = (lv.W + pl.TX - 1) / pl.TX;
     lv.nty = (lv.H + pl.TY - 1) / pl.TY;
     lv.ntz = (lv.D + pl.TZ - 1) / pl.TZ;
@@ -314,6 +326,7 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
   pl.div_lp = msda::make_fastdiv((uint32_t)(d->num_levels * d->num_points > 0
                                                 ? d->num_levels * d->num_points : 1));
   pl.tiles_per_bh = tiles;
+  pl.mul24 = mul24 ? 1 : 0;
   pl.hg_log2 = hg;
   pl.bins = tiles << hg;
   pl.upw = (msda::kGradThreads >> lay.lpu_log2) * msda::kGradRounds;

@@ -205,22 +205,29 @@ __device__ inline bool sample_rows(const BwdPlan& pl, const BwdLevel& lv, const 
   const float uy = grid_to_u(xyz[1], (float)lv.H, pl.clamp, pl.lo_g, pl.hi_g, &py);
   sm.ax = axis_from_u(ux, lv.W, px);
   sm.ay = axis_from_u(uy, lv.H, py);
-  const uint32_t W = (uint32_t)lv.W, HW = (uint32_t)lv.W * (uint32_t)lv.H;
-  uint32_t row0 = (uint32_t)lv.start + (uint32_t)sm.ay.i0 * W + (uint32_t)sm.ax.i0;
-  bool any = (sm.ax.v0 || sm.ax.v1) && (sm.ay.v0 || sm.ay.v1);
   int tz = 0;
+  bool any = (sm.ax.v0 || sm.ax.v1) && (sm.ay.v0 || sm.ay.v1);
   if constexpr (DIM == 3) {
     const float uz = grid_to_u(xyz[2], (float)lv.D, pl.clamp, pl.lo_g, pl.hi_g, &pz);
     sm.az = axis_from_u(uz, lv.D, pz);
-    row0 += (uint32_t)sm.az.i0 * HW;
     any = any && (sm.az.v0 || sm.az.v1);
     tz = any ? anchor_tile(sm.az, pl.tz_log2) : 0;
   }
-  const uint32_t off0 = vbase + row0 * rs;
+  // byte offset of the lowest corner; 24-bit multiplies when the plan allows them
+  int32_t o0;
+  if (pl.mul24) {
+    o0 = __mul24(sm.ay.i0, lv.sy) + __mul24(sm.ax.i0, (int32_t)rs);
+    if constexpr (DIM == 3) o0 += __mul24(sm.az.i0, lv.sz);
+  } else {
+    o0 = sm.ay.i0 * lv.sy + sm.ax.i0 * (int32_t)rs;
+    if constexpr (DIM == 3) o0 += sm.az.i0 * lv.sz;
+  }
+  const uint32_t off0 = vbase + lv.base + (uint32_t)o0;
 #pragma unroll
   for (int c = 0; c < (1 << DIM); ++c) {
-    const uint32_t dr = ((c & 1) ? 1u : 0u) + ((c & 2) ? W : 0u) + ((DIM == 3 && (c & 4)) ? HW : 0u);
-    off[c] = corner_valid<DIM>(c, sm) ? off0 + dr * rs : kOobOffset;
+    const uint32_t dr = ((c & 1) ? rs : 0u) + ((c & 2) ? (uint32_t)lv.sy : 0u) +
+                        ((DIM == 3 && (c & 4)) ? (uint32_t)lv.sz : 0u);
+    off[c] = corner_valid<DIM>(c, sm) ? off0 + dr : kOobOffset;
   }
   if (any) {
     const int tib = lv.tile_off + (tz * lv.nty + anchor_tile(sm.ay, pl.ty_log2)) * lv.ntx +

@@ -60,15 +60,17 @@ struct FwdLevel {
 constexpr int32_t kLvlStaged = 1;  // rows are in LDS
 constexpr int32_t kLvlMul24 = 2;   // strides and extents fit 24-bit signed multiplies
 
-// Strides of a level whose rows are sx bytes apart; kLvlMul24 when every product of an
-// index in [-2, extent + 1] and a stride fits the 24-bit multiplier.
+// Strides of a level whose rows are sx bytes apart; kLvlMul24 when every stride used and
+// every index in [-2, extent + 1] fits a signed 24-bit multiplier input.
+template <int DIM>
 __device__ inline void set_strides(FwdLevel& e, uint32_t sx) {
   const uint64_t sy = (uint64_t)e.W * sx, sz = sy * (uint64_t)e.H;
   constexpr uint64_t lim = 1u << 23;
   e.sx = (int32_t)sx;
   e.sy = (int32_t)sy;
-  e.sz = (int32_t)sz;
-  const bool m24 = sx < lim && sy < lim && sz < lim && (uint64_t)e.D + 2 < lim;
+  e.sz = DIM == 3 ? (int32_t)sz : 0;
+  const uint64_t ext = (uint64_t)max(max(e.W, e.H), e.D) + 2;
+  const bool m24 = sx < lim && sy < lim && (DIM == 2 || sz < lim) && ext < lim;
   e.flags = (e.flags & ~kLvlMul24) | (m24 ? kLvlMul24 : 0);
 }
 
@@ -89,7 +91,7 @@ __device__ inline void stage_levels(const Params& p, FwdLevel* s_lvl, uint32_t r
     }
     e.base = (uint32_t)e.start * rs;
     e.flags = 0;
-    set_strides(e, rs);
+    set_strides<DIM>(e, rs);
     s_lvl[i] = e;
   }
 }
@@ -330,7 +332,7 @@ __global__ __launch_bounds__(kFwdStageThreads) void msda_fwd_staged_kernel(const
       FwdLevel& e = s_lvl[best];
       e.flags |= kLvlStaged;
       e.base = used * lrs;
-      set_strides(e, lrs);
+      set_strides<DIM>(e, lrs);
       s_order[n] = best;
       s_pfx[n] = used * nvec;
       used += bsz;

@@ -82,6 +82,8 @@ struct BwdLevel {
   int32_t tile_off;            // index of the level's first tile within a (b, h); the
                                // coarsest level comes first so its long chunks start early
   int32_t ntiles;              // ntx * nty * ntz
+  uint32_t base;               // start * rs: byte offset of the level's first row in a (b, h) slice
+  int32_t sy, sz;              // byte strides along y and z (W * rs, H * W * rs); x is rs
 };
 
 struct BwdPlan {
@@ -110,6 +112,7 @@ struct BwdPlan {
   int32_t lpu_log2, nvec;
   int32_t clamp;
   int32_t coords_aligned;      // loc and attn are 16-byte aligned: per-batch block loads allowed
+  int32_t mul24;               // every row stride and corner index fits 24-bit multiplies
   float lo_g, hi_g;
   uint32_t value_bytes;
   uint32_t lds_g_bytes;        // bytes of the staged grad_out rows of a sub-batch

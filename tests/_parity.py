@@ -248,6 +248,23 @@ class ParitySuite:
         _, gv, gl, ga = self.run_fwd_bwd(value, shapes, loc, attn, grad_out)
         self.check_grads(value, shapes, loc, attn, grad_out, gv, gl, ga)
 
+    def test_wide_level_32bit_addressing(self) -> None:
+        """A level whose row stride along y (2D) or z (3D) exceeds 2^23 bytes: corner offsets
+        take the 32-bit multiply path instead of the 24-bit one, forward and backward."""
+        ss = [(2, 16400), (3, 5)] if self.dim == 2 else [(2, 2, 8200), (2, 3, 4)]
+        value, shapes, loc, attn = self.inputs(batch_size=1, num_queries=40, num_heads=8,
+                                               dim_per_head=32, num_levels=2, num_points=4,
+                                               spatial_shapes=ss)
+        ref = torch_ref.msda_ref(value, shapes, loc, attn)
+        out = self.fwd(*self.gpu(value), shapes, *self.gpu(loc, attn)).cpu()
+        assert max_rel(out, ref) <= FWD_TOL_F32
+        # at 16400 cells a float64 pixel coordinate differs from the fp32 one by ~1e-3 px:
+        # the brute-force oracle rounds coordinates to fp32 as the kernel does
+        assert max_rel(out, brute.fwd(value, shapes, loc, attn, coord_f32=True)) <= FWD_TOL_F32
+        grad_out = torch.randn(out.shape, generator=torch.Generator().manual_seed(3))
+        _, gv, gl, ga = self.run_fwd_bwd(value, shapes, loc, attn, grad_out)
+        self.check_grads(value, shapes, loc, attn, grad_out, gv, gl, ga)
+
     def test_empty_inputs(self) -> None:
         value, shapes, loc, attn = self.inputs(batch_size=2, num_queries=0)
         out = self.fwd(*self.gpu(value), shapes, *self.gpu(loc, attn))
