@@ -39,7 +39,7 @@ const char* dtype_name(int dt) {
 constexpr uint64_t kLim31 = 0x7FFFFFFFull;
 constexpr uint64_t kCus = 256;  // MI355X compute units: workgroups of the staged forward
 constexpr uint32_t kChunkRecords = 4096;        // records per tile-kernel chunk (rounded to S)
-constexpr uint32_t kTileLdsTarget = 52 * 1024;  // three tile workgroups per CU (160 KB LDS)
+constexpr uint32_t kTileLdsTarget = 80 * 1024 - 256;  // two tile workgroups per CU (160 KB LDS)
 constexpr uint32_t kTileLdsBudget = 160 * 1024 - 256;  // one workgroup per CU
 constexpr int kMaxBinsLds = 8192;  // bin histogram + bases in 64 KB of LDS
 
@@ -212,22 +212,21 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
                   lay.vec_bytes);
   const int s = elem_bytes(d->value_dtype);
   const int nc = 1 << d->dim;
-  const int rw = d->dim + 2;  // words per record
   if ((uint64_t)d->num_queries * d->num_points > (uint64_t)msda::kRecIdMask)
     return fail(MSDA_ERR_INVALID,
                 "backward supports Q*P up to 2^27 per launch, got Q=%lld P=%d",
                 (long long)d->num_queries, d->num_points);
-  // Tile extents and sub-batch size: start from 16x16 (2D) / 8x8x8 (3D) cells and 512
-  // records; halve S (down to 32) and then the largest tile extent until a thread owns at
-  // most kTileMaxItems (region cell, chunk) items, the region has at most 2 * kTileThreads
-  // cells, a thread stages at most kTileGradPerThread grad_out chunks and counts at most
-  // kTileRecPerThread records, and the staged grad_out rows, records, sorted entries and
-  // counters fit the LDS share of one of three workgroups per CU (or,
-  // for very wide heads, all of a CU's LDS).
+  // Tile extents and sub-batch size: start from 16x16 (2D) / 8x8x8 (3D) cells and
+  // S = kTileThreads records (one per thread); halve the largest tile extent until a thread
+  // owns at most kTileMaxItems (region cell, owner chunk) items, and lower S in steps of
+  // one wave until the sub-batch's fp32 grad_out rows, sorted entries and two counter sets
+  // fit the LDS share of one of two workgroups per CU (or, for very wide heads, all of a
+  // CU's LDS).
   const uint32_t NT = msda::kTileThreads;
-  const uint32_t grow = (uint32_t)(d->channels * s);
+  const uint32_t grow = (uint32_t)d->channels * 4u;
+  const int onv = d->channels / msda::tile_owner_vec(lay.vec_bytes / s);
   int T[3];
-  uint32_t S = 512, lds = 0;
+  uint32_t S = NT, lds = 0;
   int rcells = 0;
   auto shrink = [&]() {
     const int k = (T[2] >= T[1] && T[2] >= T[0] && T[2] > 1) ? 2 : (T[1] >= T[0] && T[1] > 1 ? 1 : 0);
@@ -235,29 +234,33 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
     T[k] /= 2;
     return true;
   };
-  // largest tile, then largest S, that meets the per-thread limits and the LDS budget
+  // largest tile, then largest S, that meets the per-thread limit and the LDS budget
   auto fit = [&](uint32_t budget) {
     T[0] = T[1] = 16;
     T[2] = 1;
     if (d->dim == 3) T[0] = T[1] = T[2] = 8;
-    S = 512;
+    S = NT;
     for (;;) {
       const int rz = d->dim == 3 ? T[2] + 1 : 1;
       rcells = (T[0] + 1) * (T[1] + 1) * rz;
-      lds = S * grow + S * nc * 8u + S * rw * 4u + (uint32_t)(rcells + 1 + NT / 64) * 4u;
-      if ((uint32_t)(rcells * lay.nvec) > msda::kTileMaxItems * NT || (uint32_t)rcells > 2 * NT) {
+      const int mi = d->dim == 2 ? msda::kTileMaxItems<2> : msda::kTileMaxItems<3>;
+      if ((uint64_t)rcells * onv > (uint64_t)mi * NT) {
         if (!shrink()) return false;
         continue;
       }
-      if (S <= msda::kTileRecPerThread * NT &&
-          S * (uint32_t)lay.nvec <= msda::kTileGradPerThread * NT && lds <= budget)
-        return true;
-      if (S > 32) {
-        S /= 2;
+      lds = S * grow + S * nc * 8u + 2u * (uint32_t)(rcells + 1) * 4u;
+      // a corner's (cell, rank) pair is packed into 16 + 16 bits
+      if (rcells >= (1 << 16) || S * nc >= (1u << 16)) {
+        if (!shrink()) return false;
+        continue;
+      }
+      if (lds <= budget) return true;
+      if (S > (uint32_t)msda::kWave) {
+        S -= (uint32_t)msda::kWave;
         continue;
       }
       if (!shrink()) return false;
-      S = 512;
+      S = NT;
     }
   };
   if (!fit(kTileLdsTarget) && !fit(kTileLdsBudget))
@@ -274,6 +277,8 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
   pl.ty_log2 = log2i(T[1]);
   pl.tz_log2 = log2i(T[2]);
   pl.div_nvec = msda::make_fastdiv((uint32_t)lay.nvec);
+  pl.onv = onv;
+  pl.div_onv = msda::make_fastdiv((uint32_t)onv);
   pl.div_rx = msda::make_fastdiv((uint32_t)(T[0] + 1));
   pl.div_rxy = msda::make_fastdiv((uint32_t)((T[0] + 1) * (T[1] + 1)));
   pl.div_tx = msda::make_fastdiv((uint32_t)T[0]);

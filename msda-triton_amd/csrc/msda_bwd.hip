@@ -540,16 +540,36 @@ __device__ inline int corner_cell(const BwdPlan& pl, const TileCoord& tc, const 
 }
 
 // ------------------------------------------------------------------ 5: tile kernel
-// One workgroup (kTileThreads threads) per chunk of a tile's records. LDS holds, per
-// sub-batch of up to S records: the records, their grad_out rows, the (weight, record)
-// entries of their corners sorted by region cell, and per-cell counts. Per sub-batch:
-//   A1. copy the records (coalesced) and clear the counters;
-//   A2. stage the grad_out rows (all loads of a thread issued before any is stored) and
-//       count corners per region cell, keeping each corner's rank;
-//   B.  exclusive scan of the per-cell counts;
-//   C.  place the entries at offset + rank;
-//   D.  the thread owning (region cell, channel chunk) sums attn*w*grad_out over its
-//       cell's entries in fp32 registers.
+// Exclusive scan, in place, of the n + 1 counters of a region by one wave; c[n] gets the
+// total. Every lane of the wave must call it.
+__device__ inline void wave_scan_counts(uint32_t* c, int n) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int per = (n + kWave - 1) / kWave;
+  const int i0 = lane * per, i1 = min(n, i0 + per);
+  uint32_t sum = 0;
+  for (int i = i0; i < i1; ++i) sum += c[i];
+  const uint32_t inc = wave_incl_scan(sum);
+  uint32_t run = inc - sum;
+  for (int i = i0; i < i1; ++i) {
+    const uint32_t v = c[i];
+    c[i] = run;
+    run += v;
+  }
+  if (lane == kWave - 1) c[n] = inc;
+}
+
+// One workgroup (kTileThreads threads) per chunk of a tile's records, in sub-batches of
+// S <= kTileThreads records; thread t owns record t of the sub-batch in registers. LDS
+// holds the sub-batch's grad_out rows widened to fp32, its (attn * corner weight, row
+// byte offset) entries sorted by region cell, and two sets of per-cell counters (one
+// being filled while the other is cleared). Per sub-batch, four barriers:
+//   1. every wave stages the grad_out rows of its 64 records (four lanes per 16-byte
+//      chunk group, the row index handed over with ds_bpermute) while each record's
+//      owner counts its corners per region cell (LDS integer atomics give the ranks);
+//   2. one wave scans the counters; the other counter set is cleared;
+//   3. owners place their entries at offset + rank and fetch the next sub-batch's record;
+//   4. the thread owning (region cell, channel chunk) sums its cell's entries into fp32
+//      registers.
 template <int DIM, typename EV, typename EC, int VEC>
 __global__ __launch_bounds__(kTileThreads, kTileWavesPerSimd) void bwd_tile_kernel(const BwdPlan pl,
                                                                 const BwdBuffers bf) {
@@ -557,10 +577,10 @@ __global__ __launch_bounds__(kTileThreads, kTileWavesPerSimd) void bwd_tile_kern
   constexpr int VB = VEC * EV::kBytes;
   constexpr int NC = 1 << DIM;
   constexpr int RW = DIM + 2;        // words per record
-  constexpr int MI = kTileMaxItems;  // owner items per thread
-  constexpr int RPT = kTileRecPerThread;
-  constexpr int GPT = kTileGradPerThread;
-  typedef typename EC::T TC;
+  constexpr int MI = kTileMaxItems<DIM>;  // owner items per thread
+  constexpr int OV = tile_owner_vec(VEC);  // channels per owner item: 16 fp32 bytes, so the
+                                           // lanes of one cell read a staged row conflict-free
+  constexpr int GB = 4;                   // grad_out chunk loads in flight per thread
   typedef typename EV::T TV;
   extern __shared__ __attribute__((aligned(16))) char s_mem[];
 
@@ -580,111 +600,145 @@ __global__ __launch_bounds__(kTileThreads, kTileWavesPerSimd) void bwd_tile_kern
   const TileCoord tc = decode_tile(pl, t);
   const BwdLevel lv = pl.lv[tc.l];
 
-  char* s_g = s_mem;                                                         // [S][C] raw rows
-  uint2* s_ent = reinterpret_cast<uint2*>(s_g + pl.lds_g_bytes);             // [S * NC]
-  uint32_t* s_rec = reinterpret_cast<uint32_t*>(s_ent + (size_t)pl.S * NC);  // [S][RW]
-  uint32_t* s_cnt = s_rec + (size_t)pl.S * RW;                               // [rcells + 1]
-  uint32_t* s_w = s_cnt + pl.rcells + 1;                                     // [NT / 64]
+  const uint32_t S = pl.S;
+  const uint32_t grow = (uint32_t)pl.C * 4u;  // bytes of one staged fp32 grad_out row
+  char* s_g = s_mem;                                                   // [S][C] fp32
+  uint2* s_ent = reinterpret_cast<uint2*>(s_g + pl.lds_g_bytes);       // [S * NC]
+  uint32_t* s_cnt2 = reinterpret_cast<uint32_t*>(s_ent + (size_t)S * NC);  // 2 x [rcells + 1]
   const int ncell_r = pl.rcells;
-  const uint32_t grow = (uint32_t)pl.C * EV::kBytes;  // bytes of one staged grad_out row
+  const uint32_t nvec = (uint32_t)pl.nvec;
+  const int tid = (int)threadIdx.x;
+  const int lane = tid & (kWave - 1), wv = tid >> 6;
   const TV* gout = static_cast<const TV*>(bf.grad_out) + ((size_t)tc.b * pl.Q * pl.H + tc.h) * pl.C;
   const size_t grad_q_stride = (size_t)pl.H * pl.C;  // elements between queries of grad_out
 
-  float acc[MI][VEC];
+  const int onv = pl.onv;
+  float acc[MI][OV];
 #pragma unroll
   for (int m = 0; m < MI; ++m)
 #pragma unroll
-    for (int k = 0; k < VEC; ++k) acc[m][k] = 0.0f;
+    for (int k = 0; k < OV; ++k) acc[m][k] = 0.0f;
 
-  for (uint32_t sb = beg; sb < end; sb += pl.S) {
-    const uint32_t nrec = min((uint32_t)pl.S, end - sb);
-    // A1. records -> LDS; clear the counters
-    for (uint32_t i = threadIdx.x; i < nrec * RW; i += NT) s_rec[i] = bf.records[(size_t)sb * RW + i];
-    for (int i = threadIdx.x; i <= ncell_r; i += NT) s_cnt[i] = 0u;
-    __syncthreads();
-
-    // A2. grad_out rows -> LDS; corner counts and ranks
-    {
-      RawVec<VB> gr[GPT];
-      const uint32_t nchunk = nrec * (uint32_t)pl.nvec;
+  for (int i = tid; i < 2 * (ncell_r + 1); i += NT) s_cnt2[i] = 0u;
+  uint32_t rec[RW];
 #pragma unroll
-      for (int k = 0; k < GPT; ++k) {
-        const uint32_t j = threadIdx.x + k * NT;
-        if (j < nchunk) {
-          const uint32_t r = fdiv(j, pl.div_nvec), ch = j - r * (uint32_t)pl.nvec;
-          const uint32_t q = fdiv(s_rec[r * RW] & kRecIdMask, pl.div_p);
-          gr[k] = glb_load<VB>(gout + (size_t)q * grad_q_stride + ch * VEC);
+  for (int k = 0; k < RW; ++k) rec[k] = 0u;
+  if ((uint32_t)tid < S && beg + (uint32_t)tid < end) {
+#pragma unroll
+    for (int k = 0; k < RW; ++k) rec[k] = bf.records[(size_t)(beg + tid) * RW + k];
+  }
+  __syncthreads();
+
+  int par = 0;
+  for (uint32_t sb = beg; sb < end; sb += S, par ^= 1) {
+    const uint32_t nrec = min(S, end - sb);
+    uint32_t* s_cnt = s_cnt2 + par * (ncell_r + 1);
+    const bool has = (uint32_t)tid < nrec;
+
+    // 1. grad_out rows -> LDS as fp32; corner ranks
+    const uint32_t q = has ? fdiv(rec[0] & kRecIdMask, pl.div_p) : 0u;
+    Sample<DIM> sm;
+    uint32_t slot[NC];  // (region cell << 16) | rank within the cell, or ~0u: no entry
+    for (uint32_t m0 = 0; m0 < nvec; m0 += GB) {
+      RawVec<VB> gr[GB];
+      uint32_t dst[GB];
+#pragma unroll
+      for (int k = 0; k < GB; ++k) {
+        const uint32_t m = m0 + (uint32_t)k;
+        dst[k] = 0xffffffffu;
+        if (m < nvec) {  // uniform
+          const uint32_t jj = m * kWave + (uint32_t)lane;
+          const uint32_t lr = fdiv(jj, pl.div_nvec), ch = jj - lr * nvec;
+          const uint32_t qq = (uint32_t)__builtin_amdgcn_ds_bpermute((int)(lr << 2), (int)q);
+          const uint32_t r = (uint32_t)wv * kWave + lr;
+          if (r < nrec) {
+            gr[k] = glb_load<VB>(gout + (size_t)qq * grad_q_stride + ch * VEC);
+            dst[k] = r * grow + ch * (VEC * 4u);
+          }
+        }
+      }
+      if (m0 == 0 && has) {
+        // the owner's corners, while the first row loads are in flight
+        sm = record_sample<DIM>(rec, lv);
+#pragma unroll
+        for (int cc = 0; cc < NC; ++cc) {
+          const int ce = corner_cell<DIM>(pl, tc, sm, cc);
+          slot[cc] = 0xffffffffu;
+          if (corner_valid<DIM>(cc, sm) && ce >= 0)
+            slot[cc] = ((uint32_t)ce << 16) | atomicAdd(&s_cnt[ce], 1u);
         }
       }
 #pragma unroll
-      for (int k = 0; k < GPT; ++k) {
-        const uint32_t j = threadIdx.x + k * NT;
-        if (j < nchunk) {
-          const uint32_t r = fdiv(j, pl.div_nvec), ch = j - r * (uint32_t)pl.nvec;
-          *reinterpret_cast<RawVec<VB>*>(s_g + r * grow + ch * VB) = gr[k];
+      for (int k = 0; k < GB; ++k) {
+        if (dst[k] == 0xffffffffu) continue;
+        float v[VEC];
+        widen<EV, VEC>(gr[k], v);
+        float* d = reinterpret_cast<float*>(s_g + dst[k]);
+        if constexpr (VEC % 4 == 0) {
+#pragma unroll
+          for (int i = 0; i < VEC; i += 4)
+            *reinterpret_cast<float4*>(d + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) d[i] = v[i];
         }
       }
     }
-    uint32_t rank[RPT][NC];
-#pragma unroll
-    for (int k = 0; k < RPT; ++k) {
-      const uint32_t r = threadIdx.x + k * NT;
-      if (r >= nrec) continue;
-      const Sample<DIM> sm = record_sample<DIM>(s_rec + r * RW, lv);
-#pragma unroll
-      for (int cc = 0; cc < NC; ++cc) {
-        const int cell = corner_cell<DIM>(pl, tc, sm, cc);
-        if (corner_valid<DIM>(cc, sm) && cell >= 0) rank[k][cc] = atomicAdd(&s_cnt[cell], 1u);
-      }
-    }
     __syncthreads();
 
-    // B. exclusive scan of the per-cell counts (rcells <= 2 * NT)
+    // 2. scan this set of counters; clear the other (last read in the previous sub-batch)
+    if (wv == 0) wave_scan_counts(s_cnt, ncell_r);
     {
-      const int i0 = 2 * (int)threadIdx.x;
-      const uint32_t v0 = i0 < ncell_r ? s_cnt[i0] : 0u;
-      const uint32_t v1 = i0 + 1 < ncell_r ? s_cnt[i0 + 1] : 0u;
-      uint32_t tot;
-      const uint32_t ex = block_excl_scan<NT>(v0 + v1, s_w, &tot);
-      if (i0 < ncell_r) s_cnt[i0] = ex;
-      if (i0 + 1 < ncell_r) s_cnt[i0 + 1] = ex + v0;
-      if (threadIdx.x == 0) s_cnt[ncell_r] = tot;
+      uint32_t* o = s_cnt2 + (par ^ 1) * (ncell_r + 1);
+      for (int i = tid; i <= ncell_r; i += NT) o[i] = 0u;
     }
     __syncthreads();
 
-    // C. place the entries
-#pragma unroll
-    for (int k = 0; k < RPT; ++k) {
-      const uint32_t r = threadIdx.x + k * NT;
-      if (r >= nrec) continue;
-      const uint32_t* rw = s_rec + r * RW;
-      const Sample<DIM> sm = record_sample<DIM>(rw, lv);
-      const float a = __builtin_bit_cast(float, rw[RW - 1]);
+    // 3. place the entries; fetch the next sub-batch's record
+    if (has) {
+      const float a = as_float(rec[RW - 1]);
 #pragma unroll
       for (int cc = 0; cc < NC; ++cc) {
-        const int cell = corner_cell<DIM>(pl, tc, sm, cc);
-        if (corner_valid<DIM>(cc, sm) && cell >= 0) {
+        if (slot[cc] != 0xffffffffu) {
           const float cw = corner_weight<DIM>(cc, sm) * a;
-          s_ent[s_cnt[cell] + rank[k][cc]] = make_uint2(__builtin_bit_cast(uint32_t, cw), r);
+          s_ent[s_cnt[slot[cc] >> 16] + (slot[cc] & 0xffffu)] = make_uint2(as_u32(cw), (uint32_t)tid * grow);
         }
+      }
+    }
+    {
+      const uint32_t nx = sb + S + (uint32_t)tid;
+      if ((uint32_t)tid < S && nx < end) {
+#pragma unroll
+        for (int k = 0; k < RW; ++k) rec[k] = bf.records[(size_t)nx * RW + k];
       }
     }
     __syncthreads();
 
-    // D. owner pass: fp32 register accumulation per (region cell, channel chunk)
+    // 4. owner pass: fp32 register accumulation per (region cell, channel chunk)
 #pragma unroll
     for (int m = 0; m < MI; ++m) {
-      const int it = (int)threadIdx.x + m * NT;
-      if (it < ncell_r * pl.nvec) {
-        const int cell = (int)fdiv((uint32_t)it, pl.div_nvec), ch = it - cell * pl.nvec;
-        const uint32_t e0 = s_cnt[cell], e1 = s_cnt[cell + 1];
+      const int it = tid + m * NT;
+      if (it < ncell_r * onv) {
+        const int ce = (int)fdiv((uint32_t)it, pl.div_onv), ch = it - ce * onv;
+        const uint32_t e0 = s_cnt[ce], e1 = s_cnt[ce + 1];
+        const char* gb = s_g + ch * (OV * 4);
         for (uint32_t e = e0; e < e1; ++e) {
           const uint2 en = s_ent[e];
-          const float cw = __builtin_bit_cast(float, en.x);
-          float gv[VEC];
-          widen<EV, VEC>(*reinterpret_cast<const RawVec<VB>*>(s_g + en.y * grow + ch * VB), gv);
+          const float cw = as_float(en.x);
+          const float* g = reinterpret_cast<const float*>(gb + en.y);
+          float gv[OV];
+          if constexpr (OV == 4) {
+            const float4 f = *reinterpret_cast<const float4*>(g);
+            gv[0] = f.x;
+            gv[1] = f.y;
+            gv[2] = f.z;
+            gv[3] = f.w;
+          } else {
 #pragma unroll
-          for (int k = 0; k < VEC; ++k) acc[m][k] = __builtin_fmaf(cw, gv[k], acc[m][k]);
+            for (int i = 0; i < OV; ++i) gv[i] = g[i];
+          }
+#pragma unroll
+          for (int k = 0; k < OV; ++k) acc[m][k] = __builtin_fmaf(cw, gv[k], acc[m][k]);
         }
       }
     }
@@ -697,8 +751,8 @@ __global__ __launch_bounds__(kTileThreads, kTileWavesPerSimd) void bwd_tile_kern
 #pragma unroll
   for (int m = 0; m < MI; ++m) {
     const int it = (int)threadIdx.x + m * NT;
-    if (it >= ncell_r * pl.nvec) continue;
-    const int cell = (int)fdiv((uint32_t)it, pl.div_nvec), ch = it - cell * pl.nvec;
+    if (it >= ncell_r * onv) continue;
+    const int cell = (int)fdiv((uint32_t)it, pl.div_onv), ch = it - cell * onv;
     const int rz = (int)fdiv((uint32_t)cell, pl.div_rxy), rxy = cell - rz * pl.RX * pl.RY;
     const int ry = (int)fdiv((uint32_t)rxy, pl.div_rx), rx = rxy - ry * pl.RX;
     const int x = tc.X0 + rx, y = tc.Y0 + ry, z = tc.Z0 + rz;
@@ -707,13 +761,12 @@ __global__ __launch_bounds__(kTileThreads, kTileWavesPerSimd) void bwd_tile_kern
     const bool interior = owned && rx > 0 && ry > 0 && (DIM == 2 || rz > 0);
     if (nch == 1 && interior) {
       const uint32_t row = (uint32_t)lv.start + ((uint32_t)z * lv.H + y) * lv.W + x;
-      store_vec<EV, VEC>(static_cast<TV*>(bf.grad_value) +
-                             (((size_t)tc.b * pl.K + row) * pl.H + tc.h) * pl.C + ch * VEC,
-                         acc[m]);
+      store_vec<EV, OV>(static_cast<TV*>(bf.grad_value) +
+                            (((size_t)tc.b * pl.K + row) * pl.H + tc.h) * pl.C + ch * OV,
+                        acc[m]);
     } else {
-      float* dst = bf.scratch + ((size_t)c * ncell_r + cell) * pl.C + ch * VEC;
-#pragma unroll
-      for (int k = 0; k < VEC; ++k) dst[k] = acc[m][k];
+      float* dst = bf.scratch + ((size_t)c * ncell_r + cell) * pl.C + ch * OV;
+      store_vec<F32, OV>(dst, acc[m]);
     }
   }
 }

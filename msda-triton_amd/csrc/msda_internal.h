@@ -9,10 +9,12 @@
 namespace msda {
 
 constexpr int kMaxLevels = 64;
-constexpr int kTileThreads = 512;     // threads of the backward tile kernel
-constexpr int kTileMaxItems = 2;      // (region cell, channel chunk) items per tile thread
-constexpr int kTileRecPerThread = 2;  // sub-batch records counted per tile thread (S <= 2*NT)
-constexpr int kTileGradPerThread = 4; // grad_out row chunks staged per tile thread
+constexpr int kTileThreads = 448;     // threads of the backward tile kernel (7 waves)
+// (region cell, 4-channel chunk) owner items per tile thread
+template <int DIM>
+constexpr int kTileMaxItems = 6;
+// channels per owner item of the tile kernel for VEC channels per value load
+constexpr int tile_owner_vec(int vec) { return vec < 4 ? vec : 4; }
 constexpr int kTileWavesPerSimd = 4;  // tile-kernel occupancy target: two workgroups per CU
 constexpr int kFillStage = 2048;      // records staged in LDS per fill round
 constexpr int kGradThreads = 256;     // threads of the backward sample-gradient kernel
@@ -94,12 +96,14 @@ struct BwdPlan {
   FastDiv div_lp;              // divisor L * P (sample index -> unit, sample)
   int32_t TX, TY, TZ;          // owned cells per tile, powers of two (TZ = 1 in 2D)
   int32_t tx_log2, ty_log2, tz_log2;
-  FastDiv div_nvec;            // divisor nvec (item -> cell, channel chunk)
+  FastDiv div_nvec;            // divisor nvec (value-load chunks per row)
+  int32_t onv;                 // owner chunks per row in the tile kernel: C / tile_owner_vec(VEC)
+  FastDiv div_onv;             // divisor onv (owner item -> cell, chunk)
   FastDiv div_rx, div_rxy;     // divisors RX and RX * RY (region cell -> rx, ry, rz)
   FastDiv div_tx, div_txy;     // divisors TX and TX * TY (owned cell -> lx, ly, lz)
   int32_t RX, RY, RZ;          // region: tile + 1 along each axis (RZ = 1 in 2D)
   int32_t cells;               // owned cells per tile: TX * TY * TZ
-  int32_t rcells;              // region cells per tile: RX * RY * RZ (<= 2 * kTileThreads)
+  int32_t rcells;              // region cells per tile: RX * RY * RZ
   int32_t tiles_per_bh;
   int32_t hg_log2;
   int32_t groups;              // (batches in launch) * H / HG
@@ -108,14 +112,14 @@ struct BwdPlan {
   int32_t bins;                // tiles_per_bh * HG; bin = tile_in_bh * HG + head_in_group
   uint32_t T;                  // groups * bins: tiles of this launch
   uint32_t R;                  // records per chunk (multiple of S)
-  uint32_t S;                  // records per LDS sub-batch of the tile kernel
+  uint32_t S;                  // records per LDS sub-batch of the tile kernel (<= kTileThreads)
   int32_t lpu_log2, nvec;
   int32_t clamp;
   int32_t coords_aligned;      // loc and attn are 16-byte aligned: per-batch block loads allowed
   int32_t mul24;               // every row stride and corner index fits 24-bit multiplies
   float lo_g, hi_g;
   uint32_t value_bytes;
-  uint32_t lds_g_bytes;        // bytes of the staged grad_out rows of a sub-batch
+  uint32_t lds_g_bytes;        // bytes of the staged fp32 grad_out rows of a sub-batch
   uint32_t lds_bytes;          // total dynamic LDS of the tile kernel
   uint32_t max_chunks;         // upper bound of the chunk count
   uint32_t grid_chunks;        // tile-kernel grid: max_chunks rounded up to 8 (one per XCD)
