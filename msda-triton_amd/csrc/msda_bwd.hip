@@ -540,6 +540,21 @@ __device__ inline int corner_cell(const BwdPlan& pl, const TileCoord& tc, const 
 }
 
 // ------------------------------------------------------------------ 5: tile kernel
+// N fp32 values from LDS (one 16-byte read for N == 4).
+template <int N>
+__device__ inline void lds_f32(const char* p, float (&v)[N]) {
+  if constexpr (N == 4) {
+    const float4 f = *reinterpret_cast<const float4*>(p);
+    v[0] = f.x;
+    v[1] = f.y;
+    v[2] = f.z;
+    v[3] = f.w;
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = reinterpret_cast<const float*>(p)[i];
+  }
+}
+
 // Exclusive scan, in place, of the n + 1 counters of a region by one wave; c[n] gets the
 // total. Every lane of the wave must call it.
 __device__ inline void wave_scan_counts(uint32_t* c, int n) {
@@ -722,23 +737,27 @@ __global__ __launch_bounds__(kTileThreads, kTileWavesPerSimd) void bwd_tile_kern
         const int ce = (int)fdiv((uint32_t)it, pl.div_onv), ch = it - ce * onv;
         const uint32_t e0 = s_cnt[ce], e1 = s_cnt[ce + 1];
         const char* gb = s_g + ch * (OV * 4);
-        for (uint32_t e = e0; e < e1; ++e) {
+        // four entries per step: their entry and row reads are independent, so their LDS
+        // latencies overlap
+        uint32_t e = e0;
+        for (; e + 4 <= e1; e += 4) {
+          uint2 en[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) en[j] = s_ent[e + j];
+          float gv[4][OV];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) lds_f32<OV>(gb + en[j].y, gv[j]);
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int k = 0; k < OV; ++k) acc[m][k] = __builtin_fmaf(as_float(en[j].x), gv[j][k], acc[m][k]);
+        }
+        for (; e < e1; ++e) {
           const uint2 en = s_ent[e];
-          const float cw = as_float(en.x);
-          const float* g = reinterpret_cast<const float*>(gb + en.y);
           float gv[OV];
-          if constexpr (OV == 4) {
-            const float4 f = *reinterpret_cast<const float4*>(g);
-            gv[0] = f.x;
-            gv[1] = f.y;
-            gv[2] = f.z;
-            gv[3] = f.w;
-          } else {
+          lds_f32<OV>(gb + en.y, gv);
 #pragma unroll
-            for (int i = 0; i < OV; ++i) gv[i] = g[i];
-          }
-#pragma unroll
-          for (int k = 0; k < OV; ++k) acc[m][k] = __builtin_fmaf(cw, gv[k], acc[m][k]);
+          for (int k = 0; k < OV; ++k) acc[m][k] = __builtin_fmaf(as_float(en.x), gv[k], acc[m][k]);
         }
       }
     }
