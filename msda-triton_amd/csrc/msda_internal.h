@@ -9,10 +9,10 @@
 namespace msda {
 
 constexpr int kMaxLevels = 64;
-constexpr int kTileThreads = 448;     // threads of the backward tile kernel (7 waves)
+constexpr int kTileThreads = 512;     // threads of the backward tile kernel (8 waves)
 // (region cell, 4-channel chunk) owner items per tile thread
 template <int DIM>
-constexpr int kTileMaxItems = 6;
+constexpr int kTileMaxItems = 5;
 // channels per owner item of the tile kernel for VEC channels per value load
 constexpr int tile_owner_vec(int vec) { return vec < 4 ? vec : 4; }
 constexpr int kTileWavesPerSimd = 4;  // tile-kernel occupancy target: two workgroups per CU
