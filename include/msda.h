@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define MSDA_ABI_VERSION 1
+#define MSDA_ABI_VERSION 2
 
 typedef enum msda_dtype {
   MSDA_F32 = 0,
@@ -81,9 +81,23 @@ const char* msda_last_error(void);
 int msda_validate(const msda_desc* desc);
 
 /*
+ * Bytes of optional device workspace that lets msda_fwd gather from a head-major copy of
+ * value (B, H, K, C): returned when value rows are shorter than a 128-byte line, there is
+ * more than one head, the keys' line footprint exceeds one XCD's 4 MB L2 and the gathers
+ * outnumber the keys at least eightfold (e.g. 76.7 MB for the 3D 4-level workload), else 0.
+ * No counterpart in the reference, whose kernels always read the (B, K, H, C) layout.
+ */
+size_t msda_fwd_workspace_bytes(const msda_desc* desc);
+
+/*
  * Forward: output = sum_l sum_p attn[b,q,h,l,p] * sample(value[b, level l, h, :], loc[b,q,h,l,p])
  * with bilinear (dim 2) or trilinear (dim 3) sampling, zero padding outside the level,
  * align_corners=False, fp32 accumulation, and output rounded once to value_dtype.
+ *
+ * `workspace` is optional: with at least msda_fwd_workspace_bytes() bytes (aligned to 16
+ * bytes) the call first copies value into it in head-major order and gathers from the
+ * copy; with NULL or fewer bytes it gathers from value directly. The output is the same
+ * either way, bit for bit.
  *
  * Replaces the reference's _fwd_kernel_2d launch and permute/cast epilogue
  * (src/msda_triton/triton/msda_2d.py:606-651) and the 3D equivalent
@@ -96,11 +110,14 @@ int msda_fwd(const msda_desc* desc,
              const void* sampling_locations,
              const void* attention_weights,
              void* output,
+             void* workspace,
+             size_t workspace_bytes,
              void* stream);
 
 /*
  * Bytes of device workspace msda_bwd needs for this descriptor and these level shapes
- * (0 when there is nothing to sample). host_spatial_shapes is a HOST array of L*dim int32
+ * (0 when there is nothing to sample; it includes the head-major value copy described at
+ * msda_fwd_workspace_bytes when that applies). host_spatial_shapes is a HOST array of L*dim int32
  * laid out like spatial_shapes; the backward plans its spatial tiling from it. Returns 0
  * and sets msda_last_error() if the descriptor or shapes are invalid.
  */

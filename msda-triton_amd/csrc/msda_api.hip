@@ -42,6 +42,7 @@ constexpr uint32_t kChunkRecords = 4096;        // records per tile-kernel chunk
 constexpr uint32_t kTileLdsTarget = 80 * 1024 - 256;  // two tile workgroups per CU (160 KB LDS)
 constexpr uint32_t kTileLdsBudget = 160 * 1024 - 256;  // one workgroup per CU
 constexpr int kMaxBinsLds = 8192;  // bin histogram + bases in 64 KB of LDS
+constexpr uint64_t kL2Bytes = 4ull << 20;  // L2 of one XCD
 
 // Lanes per unit and per-lane vector width for one C-channel value row.
 struct Layout {
@@ -136,6 +137,19 @@ int64_t batches_per_launch(const msda_desc* d, const Layout& lay) {
   if (per_b_lanes) nb = min64(nb, (int64_t)(kLim31 / per_b_lanes));
   if (per_b_rec) nb = min64(nb, (int64_t)(kLim31 / per_b_rec));
   return nb < 1 ? 1 : nb;
+}
+
+// Whether the kernels should gather from a head-major (B, H, K, C) copy of value. In the
+// (B, K, H, C) layout a row shorter than a 128-byte line shares its line with other heads,
+// and a head's rows touch K lines; once those exceed an XCD's L2, random gathers miss on
+// most lines. In the copy one head's rows are contiguous (half the footprint for 64-byte
+// rows) and the two x-neighbours of a corner pair often share a line. The copy costs a read
+// and a write of value, so it is made only when the gathers are many times larger.
+bool use_head_major(const msda_desc* d) {
+  const uint64_t row = (uint64_t)d->channels * elem_bytes(d->value_dtype);
+  const uint64_t gathers = (uint64_t)d->num_queries * d->num_levels * d->num_points << d->dim;
+  return d->num_heads > 1 && row <= 64 && (uint64_t)d->num_keys * 128 > kL2Bytes &&
+         gathers >= 8 * (uint64_t)d->num_keys;
 }
 
 void fill_params(const msda_desc* d, const Layout& lay, int64_t nb, msda::Params* p) {
@@ -293,10 +307,12 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
   pl.lds_bytes = lds;
   // tiles of the coarsest level first: its chunks are the longest, so they start early
   int tiles = 0;
-  bool mul24 = (uint64_t)d->num_heads * d->channels * s < (1u << 23);
+  const bool head_major = use_head_major(d);
+  bool mul24 = (uint64_t)(head_major ? 1 : d->num_heads) * d->channels * s < (1u << 23);
   for (int l = d->num_levels - 1; l >= 0; --l) {
     msda::BwdLevel& lv = pl.lv[l];
-    const uint64_t rsb = (uint64_t)d->num_heads * d->channels * s;  // bytes between rows of K
+    // bytes between rows of K (one head's rows are contiguous in the head-major copy)
+    const uint64_t rsb = (uint64_t)(head_major ? 1 : d->num_heads) * d->channels * s;
     lv.base = (uint32_t)((uint64_t)lv.start * rsb);
     lv.sy = (int32_t)((uint64_t)lv.W * rsb);
     lv.sz = (int32_t)((uint64_t)lv.W * lv.H * rsb);
@@ -332,6 +348,7 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
                                                 ? d->num_levels * d->num_points : 1));
   pl.tiles_per_bh = tiles;
   pl.mul24 = mul24 ? 1 : 0;
+  pl.head_major = head_major ? 1 : 0;
   pl.hg_log2 = hg;
   pl.bins = tiles << hg;
   pl.upw = (msda::kGradThreads >> lay.lpu_log2) * msda::kGradRounds;
@@ -376,6 +393,8 @@ void carve(char* ws, const msda::BwdSizes& z, msda::BwdBuffers* bf) {
   bf->records = reinterpret_cast<uint32_t*>(p);
   p += al(z.record_words * 4);
   bf->scratch = reinterpret_cast<float*>(p);
+  p += al(z.scratch_floats * 4);
+  bf->value_h = z.value_h_bytes ? p : nullptr;
 }
 
 }  // namespace
@@ -391,9 +410,22 @@ int msda_validate(const msda_desc* desc) {
   return validate(desc);
 }
 
+size_t msda_fwd_workspace_bytes(const msda_desc* d) {
+  g_err[0] = 0;
+  if (validate(d)) return 0;
+  if (!use_head_major(d) || d->batch == 0 || d->num_queries == 0) return 0;
+  Layout lay;
+  const void* none[1] = {nullptr};
+  if (choose_layout(d, none, 0, &lay)) return 0;
+  const int64_t nb = batches_per_launch(d, lay);
+  const int64_t bmax = d->batch < nb ? d->batch : nb;
+  return (size_t)bmax * (size_t)d->num_keys * d->num_heads * d->channels * elem_bytes(d->value_dtype);
+}
+
 int msda_fwd(const msda_desc* d, const void* value, const int32_t* spatial_shapes,
              const int32_t* level_start, const void* sampling_locations,
-             const void* attention_weights, void* output, void* stream) {
+             const void* attention_weights, void* output, void* workspace,
+             size_t workspace_bytes, void* stream) {
   g_err[0] = 0;
   int rc = validate(d);
   if (rc) return rc;
@@ -428,6 +460,16 @@ int msda_fwd(const msda_desc* d, const void* value, const int32_t* spatial_shape
     p.shapes = spatial_shapes;
     p.starts = level_start;
     p.coords_aligned = aligned(p.loc, 16) && aligned(p.attn, 16);
+    // head-major copy of this launch's value slice when it pays and the workspace holds it
+    const uint64_t vbytes = (uint64_t)bc * kv * sv;
+    if (use_head_major(d) && workspace && workspace_bytes >= vbytes &&
+        aligned(workspace, lay.vec_bytes)) {
+      hipError_t e = msda::launch_head_major(p.value, workspace, (uint32_t)bc, (uint32_t)d->num_keys,
+                                             (uint32_t)d->num_heads, (uint32_t)(d->channels * sv),
+                                             lay.vec_bytes, static_cast<hipStream_t>(stream));
+      if (e != hipSuccess) return fail(MSDA_ERR_HIP, "msda_fwd relayout failed: %s", hipGetErrorString(e));
+      p.value_h = workspace;
+    }
     // Staged kernel: one workgroup per CU, each (batch, head) slice split into query
     // ranges; used when every workgroup gets enough queries to amortise its LDS copy.
     const uint64_t slices = (uint64_t)bc * d->num_heads;
@@ -511,6 +553,12 @@ int msda_bwd(const msda_desc* d, const int32_t* host_spatial_shapes, const void*
     bf.grad_attn = static_cast<char*>(grad_attention_weights) + (uint64_t)b0 * qh * LP * sc;
     pl.coords_aligned = aligned(bf.loc, 16) && aligned(bf.attn, 16) && aligned(bf.grad_loc, 16) &&
                         aligned(bf.grad_attn, 16);
+    if (pl.head_major) {
+      hipError_t e = msda::launch_head_major(bf.value, const_cast<void*>(bf.value_h), (uint32_t)bc,
+                                             (uint32_t)d->num_keys, (uint32_t)d->num_heads,
+                                             (uint32_t)(d->channels * sv), hp.lay.vec_bytes, st);
+      if (e != hipSuccess) return fail(MSDA_ERR_HIP, "msda_bwd relayout failed: %s", hipGetErrorString(e));
+    }
     hipError_t e = msda::run_bwd(pl, bf, d->dim, d->value_dtype, d->coord_dtype,
                                  hp.lay.vec_bytes, st);
     if (e != hipSuccess) return fail(MSDA_ERR_HIP, "msda_bwd launch failed: %s", hipGetErrorString(e));

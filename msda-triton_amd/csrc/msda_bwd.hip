@@ -266,16 +266,18 @@ __global__ __launch_bounds__(kGradThreads) void bwd_grad_kernel(const BwdPlan pl
   const uint32_t gpw = (uint32_t)kGradThreads >> lg;  // unit groups per workgroup
   const uint32_t units = min((uint32_t)pl.upw, (pl.Q << pl.hg_log2) - w * (uint32_t)pl.upw);
   const int LP = pl.L * pl.P;
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc(bf.value, pl.value_bytes);
-  const uint32_t rs = (uint32_t)pl.H * (uint32_t)pl.C * EV::kBytes;  // bytes between rows of K
+  const bool hm = pl.head_major != 0;
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(hm ? bf.value_h : bf.value, pl.value_bytes);
+  // bytes between rows of K: one head's rows are contiguous in the head-major copy
+  const uint32_t rs = (hm ? 1u : (uint32_t)pl.H) * (uint32_t)pl.C * EV::kBytes;
 #pragma unroll 1
   for (uint32_t wi = threadIdx.x >> lg; wi < units; wi += gpw) {
     const BinUnit bu = bin_unit(pl, g, w, wi);
     RawVec<VB> gr = {};
     if (act) gr = glb_load<VB>(static_cast<const TV*>(bf.grad_out) + bu.bqh * pl.C + lane * VEC);
-    const uint32_t vbase =
-        ((bu.b * (uint32_t)pl.K * (uint32_t)pl.H + bu.h) * (uint32_t)pl.C + (act ? lane : 0u) * VEC) *
-        EV::kBytes;
+    const uint32_t slice = hm ? (bu.b * (uint32_t)pl.H + bu.h) * (uint32_t)pl.K * (uint32_t)pl.C
+                              : (bu.b * (uint32_t)pl.K * (uint32_t)pl.H + bu.h) * (uint32_t)pl.C;
+    const uint32_t vbase = (slice + (act ? lane : 0u) * VEC) * EV::kBytes;
     const TC* locp = static_cast<const TC*>(bf.loc) + bu.bqh * LP * DIM;
     const TC* attp = static_cast<const TC*>(bf.attn) + bu.bqh * LP;
     TC* glp = static_cast<TC*>(bf.grad_loc) + bu.bqh * LP * DIM;
@@ -947,9 +949,11 @@ BwdSizes bwd_sizes(const BwdPlan& pl, uint64_t samples, int dim) {
   z.chunk_tile = pl.max_chunks;
   z.record_words = (samples > 0 ? samples : 1) * (uint64_t)(dim + 2);
   z.scratch_floats = (uint64_t)pl.max_chunks * pl.rcells * pl.C;
+  z.value_h_bytes = pl.head_major ? (uint64_t)pl.value_bytes : 0u;
   auto al = [](uint64_t b) { return (b + 255) & ~(uint64_t)255; };
   z.total_bytes = al(z.counts * 4) + al(z.bin_start * 4) + al(z.chunk_off * 4) +
-                  al(z.chunk_tile * 4) + al(z.record_words * 4) + al(z.scratch_floats * 4);
+                  al(z.chunk_tile * 4) + al(z.record_words * 4) + al(z.scratch_floats * 4) +
+                  al(z.value_h_bytes);
   return z;
 }
 

@@ -74,6 +74,16 @@ __device__ inline void set_strides(FwdLevel& e, uint32_t sx) {
   e.flags = (e.flags & ~kLvlMul24) | (m24 ? kLvlMul24 : 0);
 }
 
+// Bytes between consecutive rows of K, and the first byte of the (b, h) slice, in the
+// (B, K, H, C) value or its head-major (B, H, K, C) copy.
+__device__ inline uint32_t row_stride(const Params& p, int eb) {
+  return (p.value_h ? 1u : (uint32_t)p.H) * (uint32_t)p.C * (uint32_t)eb;
+}
+__device__ inline uint32_t slice_base(const Params& p, uint32_t b, uint32_t h, int eb) {
+  return (p.value_h ? (b * (uint32_t)p.H + h) * (uint32_t)p.K : b * (uint32_t)p.K * (uint32_t)p.H + h) *
+         (uint32_t)p.C * (uint32_t)eb;
+}
+
 // Level table for global reads with rows rs bytes apart.
 template <int DIM>
 __device__ inline void stage_levels(const Params& p, FwdLevel* s_lvl, uint32_t rs) {
@@ -165,9 +175,9 @@ __device__ inline void unit_forward(const Params& p, const FwdLevel* s_lvl, cons
   const int LP = p.L * p.P;
   const TC* locp = static_cast<const TC*>(p.loc) + (size_t)bqh * (LP * DIM);
   const TC* attp = static_cast<const TC*>(p.attn) + (size_t)bqh * LP;
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.value, p.value_bytes);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.value_h ? p.value_h : p.value, p.value_bytes);
   const uint32_t lane_off = lane * VB;
-  const uint32_t vbase = ((b * (uint32_t)p.K * (uint32_t)p.H + h) * (uint32_t)p.C) * EV::kBytes + lane_off;
+  const uint32_t vbase = slice_base(p, b, h, EV::kBytes) + lane_off;
 
 #pragma unroll
   for (int i = 0; i < VEC; ++i) acc[i] = 0.0f;
@@ -285,7 +295,7 @@ __device__ inline void unit_forward(const Params& p, const FwdLevel* s_lvl, cons
 template <int DIM, typename EV, typename EC, int VEC, int PT>
 __global__ __launch_bounds__(kBlock) void msda_fwd_kernel(const Params p) {
   __shared__ FwdLevel s_lvl[kMaxLevels];
-  stage_levels<DIM>(p, s_lvl, (uint32_t)p.H * (uint32_t)p.C * EV::kBytes);
+  stage_levels<DIM>(p, s_lvl, row_stride(p, EV::kBytes));
   __syncthreads();
   Unit u;
   if (!decode_unit(p, u)) return;
@@ -308,7 +318,7 @@ __global__ __launch_bounds__(kFwdStageThreads) void msda_fwd_staged_kernel(const
   __shared__ uint32_t s_pfx[kMaxLevels + 1];  // their first piece in the flat staging index
   __shared__ int32_t s_nst;
   const uint32_t lrs = (uint32_t)p.C * EV::kBytes;  // bytes per staged row
-  stage_levels<DIM>(p, s_lvl, (uint32_t)p.H * (uint32_t)p.C * EV::kBytes);
+  stage_levels<DIM>(p, s_lvl, row_stride(p, EV::kBytes));
   __syncthreads();
   const uint32_t nvec = (uint32_t)p.nvec;
   if (threadIdx.x == 0) {
@@ -353,9 +363,9 @@ __global__ __launch_bounds__(kFwdStageThreads) void msda_fwd_staged_kernel(const
   // copy the staged levels' rows of (b, h): every load of a thread is issued before any of
   // its stores
   {
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.value, p.value_bytes);
-    const uint32_t rs = (uint32_t)p.H * (uint32_t)p.C * EV::kBytes;
-    const uint32_t vrow0 = ((b * (uint32_t)p.K * (uint32_t)p.H + h) * (uint32_t)p.C) * EV::kBytes;
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.value_h ? p.value_h : p.value, p.value_bytes);
+    const uint32_t rs = row_stride(p, EV::kBytes);
+    const uint32_t vrow0 = slice_base(p, b, h, EV::kBytes);
     const int nst = s_nst;
     const uint32_t total = s_pfx[nst];
     constexpr int KB = 8;
@@ -454,6 +464,43 @@ static LaunchFn pick_types(int vdt, int cdt, int vec_bytes, bool staged) {
   if (vdt == 2 && cdt == 2) return pick_vec<DIM, BF16, BF16>(vec_bytes, staged);
   if (vdt == 2 && cdt == 0) return pick_vec<DIM, BF16, F32>(vec_bytes, staged);
   return nullptr;
+}
+
+// Head-major copy: thread i moves chunk i of value in (b, k, h, chunk) order, so reads are
+// contiguous and the 2 keys x H heads of a wave write whole 128-byte lines per head.
+template <int VB>
+__global__ __launch_bounds__(kBlock) void head_major_kernel(const char* __restrict__ src,
+                                                           char* __restrict__ dst, uint32_t n,
+                                                           FastDiv div_c, FastDiv div_hc,
+                                                           FastDiv div_khc, uint32_t K,
+                                                           uint32_t H, uint32_t row) {
+  const uint32_t stride = gridDim.x * kBlock;
+  for (uint32_t i = blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+    const uint32_t b = fdiv(i, div_khc), r0 = i - b * div_khc.d;
+    const uint32_t k = fdiv(r0, div_hc), r1 = r0 - k * div_hc.d;
+    const uint32_t h = fdiv(r1, div_c), c = r1 - h * div_c.d;
+    const RawVec<VB> v = *reinterpret_cast<const RawVec<VB>*>(src + (size_t)i * VB);
+    *reinterpret_cast<RawVec<VB>*>(dst + ((size_t)(b * H + h) * K + k) * row + (size_t)c * VB) = v;
+  }
+}
+
+hipError_t launch_head_major(const void* src, void* dst, uint32_t B, uint32_t K, uint32_t H,
+                             uint32_t row_bytes, int vec_bytes, hipStream_t s) {
+  const uint32_t cpr = row_bytes / (uint32_t)vec_bytes;  // chunks per row
+  const uint64_t n = (uint64_t)B * K * H * cpr;
+  if (n == 0) return hipSuccess;
+  const FastDiv dc = make_fastdiv(cpr), dhc = make_fastdiv(H * cpr), dkhc = make_fastdiv(K * H * cpr);
+  const uint32_t blocks = (uint32_t)((n + kBlock - 1) / kBlock < 8192 ? (n + kBlock - 1) / kBlock : 8192);
+  const char* sp = static_cast<const char*>(src);
+  char* dp = static_cast<char*>(dst);
+  switch (vec_bytes) {
+    case 16: hipLaunchKernelGGL(head_major_kernel<16>, dim3(blocks), dim3(kBlock), 0, s, sp, dp, (uint32_t)n, dc, dhc, dkhc, K, H, row_bytes); break;
+    case 8: hipLaunchKernelGGL(head_major_kernel<8>, dim3(blocks), dim3(kBlock), 0, s, sp, dp, (uint32_t)n, dc, dhc, dkhc, K, H, row_bytes); break;
+    case 4: hipLaunchKernelGGL(head_major_kernel<4>, dim3(blocks), dim3(kBlock), 0, s, sp, dp, (uint32_t)n, dc, dhc, dkhc, K, H, row_bytes); break;
+    case 2: hipLaunchKernelGGL(head_major_kernel<2>, dim3(blocks), dim3(kBlock), 0, s, sp, dp, (uint32_t)n, dc, dhc, dkhc, K, H, row_bytes); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 LaunchFn get_fwd_launcher(int dim, int vdt, int cdt, int vec_bytes, bool staged) {

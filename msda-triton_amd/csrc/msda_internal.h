@@ -53,9 +53,17 @@ struct Params {
   uint32_t splits;         // workgroups per (batch, head)
   uint32_t qper;           // queries per workgroup
   uint32_t stage_bytes;    // LDS bytes for staged rows
+  // head-major copy of value, (Bc, H, K, C), or nullptr: rows are then read from it with
+  // the rows of one head contiguous
+  const void* value_h;
 };
 
 using LaunchFn = hipError_t (*)(const Params&, hipStream_t);
+
+// Copy value (B, K, H, row_bytes) into head-major order (B, H, K, row_bytes), vec_bytes
+// (16, 8, 4 or 2, dividing row_bytes and the pointers' alignment) per thread and load.
+hipError_t launch_head_major(const void* src, void* dst, uint32_t B, uint32_t K, uint32_t H,
+                             uint32_t row_bytes, int vec_bytes, hipStream_t s);
 
 // Forward launcher for (dim, value dtype, coord dtype, bytes per lane load), or nullptr.
 // `staged` selects the kernel that serves small levels from LDS (Params.splits/qper set).
@@ -117,6 +125,7 @@ struct BwdPlan {
   int32_t clamp;
   int32_t coords_aligned;      // loc and attn are 16-byte aligned: per-batch block loads allowed
   int32_t mul24;               // every row stride and corner index fits 24-bit multiplies
+  int32_t head_major;          // the sample-gradient kernel reads BwdBuffers::value_h
   float lo_g, hi_g;
   uint32_t value_bytes;
   uint32_t lds_g_bytes;        // bytes of the staged fp32 grad_out rows of a sub-batch
@@ -127,6 +136,7 @@ struct BwdPlan {
 
 struct BwdBuffers {
   const void* value;
+  const void* value_h;   // head-major copy of value (B, H, K, C) when the plan says so
   const void* loc;
   const void* attn;
   const void* grad_out;
@@ -143,6 +153,7 @@ struct BwdBuffers {
 
 struct BwdSizes {
   uint64_t counts, bin_start, chunk_off, chunk_tile, record_words, scratch_floats;
+  uint64_t value_h_bytes;  // head-major value copy (0 when the plan does not use one)
   uint64_t total_bytes;
 };
 

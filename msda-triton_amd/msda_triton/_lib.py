@@ -12,7 +12,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libmsda_hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 MSDA_F32, MSDA_F16, MSDA_BF16 = 0, 1, 2
 MSDA_OK, MSDA_ERR_INVALID, MSDA_ERR_DTYPE, MSDA_ERR_WORKSPACE, MSDA_ERR_HIP = range(5)
@@ -21,6 +21,7 @@ EXPORTED_SYMBOLS = (
     "msda_abi_version",
     "msda_last_error",
     "msda_validate",
+    "msda_fwd_workspace_bytes",
     "msda_fwd",
     "msda_bwd_workspace_bytes",
     "msda_bwd",
@@ -75,7 +76,9 @@ def load() -> ctypes.CDLL:
         lib.msda_last_error.restype = ctypes.c_char_p
         lib.msda_validate.argtypes = [dp]
         lib.msda_validate.restype = ctypes.c_int
-        lib.msda_fwd.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp]
+        lib.msda_fwd_workspace_bytes.argtypes = [dp]
+        lib.msda_fwd_workspace_bytes.restype = ctypes.c_size_t
+        lib.msda_fwd.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, ctypes.c_size_t, vp]
         lib.msda_fwd.restype = ctypes.c_int
         lib.msda_bwd_workspace_bytes.argtypes = [dp, vp]
         lib.msda_bwd_workspace_bytes.restype = ctypes.c_size_t

@@ -197,10 +197,14 @@ def forward(dim: int, value: torch.Tensor, levels: Levels, loc: torch.Tensor, at
     num_queries = loc.shape[1]
     out = torch.empty((bsz, num_queries, num_heads * ch), device=value.device, dtype=value.dtype)
     desc = make_desc(dim, value_c, loc_c, cdt, clamp_grid, clamp_eps)
+    # optional workspace: a head-major copy of value for large, line-sharing value slices
+    ws_bytes = int(lib.msda_fwd_workspace_bytes(ctypes.byref(desc)))
+    ws = torch.empty(ws_bytes, device=value.device, dtype=torch.uint8) if ws_bytes else None
     with torch.cuda.device(value.device):
         rc = lib.msda_fwd(ctypes.byref(desc), value_c.data_ptr(), levels.spatial.data_ptr(),
                           levels.starts.data_ptr(), loc_c.data_ptr(), attn_c.data_ptr(),
-                          out.data_ptr(), _stream(value.device))
+                          out.data_ptr(), ws.data_ptr() if ws is not None else None, ws_bytes,
+                          _stream(value.device))
     _lib.check(rc, "msda_fwd")
     return out, value_c, loc_c, attn_c
 

@@ -52,8 +52,9 @@ def _shapes(vals):
 def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     declared = _declared_functions()
-    assert set(declared) >= {"msda_fwd", "msda_bwd", "msda_bwd_workspace_bytes",
-                             "msda_validate", "msda_last_error", "msda_abi_version"}
+    assert set(declared) >= {"msda_fwd", "msda_fwd_workspace_bytes", "msda_bwd",
+                             "msda_bwd_workspace_bytes", "msda_validate", "msda_last_error",
+                             "msda_abi_version"}
     for name in declared:
         assert hasattr(lib, name), f"{name} declared in msda.h but not exported"
     assert set(_lib.EXPORTED_SYMBOLS) <= set(declared)
@@ -115,16 +116,35 @@ def test_bwd_workspace_bytes_host_only():
     assert lib.msda_bwd_workspace_bytes(ctypes.byref(d3), _shapes(s3)) > 0
 
 
+def test_fwd_workspace_bytes_rule():
+    """The head-major value copy is requested only where rows share 128-byte lines across
+    heads, the line footprint exceeds an XCD's L2 and gathers dominate (host-only)."""
+    lib = _lib.load()
+    c2 = _desc()
+    assert lib.msda_fwd_workspace_bytes(ctypes.byref(c2)) == 0          # 2.5 MB of lines: fits L2
+    c5 = _desc(dim=3, batch=1, num_keys=149760, num_queries=32768, num_points=8)
+    assert lib.msda_fwd_workspace_bytes(ctypes.byref(c5)) == 149760 * 8 * 32 * 2
+    c5_f32 = _desc(dim=3, batch=1, num_keys=149760, num_queries=32768, num_points=8,
+                   value_dtype=_lib.MSDA_F32, coord_dtype=_lib.MSDA_F32)
+    assert lib.msda_fwd_workspace_bytes(ctypes.byref(c5_f32)) == 0      # 128-byte rows
+    c5_few = _desc(dim=3, batch=1, num_keys=149760, num_queries=300, num_points=8)
+    assert lib.msda_fwd_workspace_bytes(ctypes.byref(c5_few)) == 0      # copy would not pay
+    c5_h1 = _desc(dim=3, batch=1, num_keys=149760, num_queries=32768, num_points=8, num_heads=1)
+    assert lib.msda_fwd_workspace_bytes(ctypes.byref(c5_h1)) == 0       # already head-major
+    assert lib.msda_fwd_workspace_bytes(ctypes.byref(_desc(dim=5))) == 0
+    assert _lib.last_error() != ""
+
+
 def test_entry_points_reject_bad_descriptors_before_any_device_work():
     lib = _lib.load()
     d = _desc(dim=5)
-    rc = lib.msda_fwd(ctypes.byref(d), None, None, None, None, None, None, None)
+    rc = lib.msda_fwd(ctypes.byref(d), None, None, None, None, None, None, None, 0, None)
     assert rc == _lib.MSDA_ERR_INVALID
     rc = lib.msda_bwd(ctypes.byref(d), None, None, None, None, None, None, None, None, None, 0,
                       None)
     assert rc == _lib.MSDA_ERR_INVALID
     d = _desc()
-    rc = lib.msda_fwd(ctypes.byref(d), None, None, None, None, None, None, None)
+    rc = lib.msda_fwd(ctypes.byref(d), None, None, None, None, None, None, None, 0, None)
     assert rc == _lib.MSDA_ERR_INVALID and "NULL" in _lib.last_error()
 
 
