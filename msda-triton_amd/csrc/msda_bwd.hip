@@ -457,8 +457,9 @@ __global__ __launch_bounds__(kBlock) void bwd_fill_kernel(const BwdPlan pl, cons
       const uint32_t nr = min((uint32_t)kFillStage, n - r0);
       for (uint32_t i = lb0 + threadIdx.x; i < lb1; i += kBlock) s_cnt[i] = 0;
       __syncthreads();
-      // rank each sample of the round within its bin
+      // rank each sample of the round within its bin; its record stays in registers
       uint32_t key[KP];
+      uint32_t rw[KP][RW];
 #pragma unroll
       for (int k = 0; k < KP; ++k) {
         key[k] = 0xffffffffu;
@@ -474,6 +475,11 @@ __global__ __launch_bounds__(kBlock) void bwd_fill_kernel(const BwdPlan pl, cons
         if (!sample_tile<DIM>(pl, lv, static_cast<const TC*>(bf.loc) + si * DIM, u, &flags, &tib)) continue;
         const uint32_t bin = ((uint32_t)tib << pl.hg_log2) | bu.hsub;
         key[k] = (bin << 16) | atomicAdd(&s_cnt[bin], 1u);
+        rw[k][0] = (bu.q * (uint32_t)pl.P + p) | flags;
+        rw[k][1] = as_u32(u[0]);
+        rw[k][2] = as_u32(u[1]);
+        if constexpr (DIM == 3) rw[k][3] = as_u32(u[2]);
+        rw[k][RW - 1] = as_u32((float)static_cast<const TC*>(bf.attn)[si]);
       }
       __syncthreads();
       // exclusive scan of the round's counts over the level's bins
@@ -492,20 +498,9 @@ __global__ __launch_bounds__(kBlock) void bwd_fill_kernel(const BwdPlan pl, cons
       for (int k = 0; k < KP; ++k) {
         if (key[k] == 0xffffffffu) continue;
         const uint32_t bin = key[k] >> 16, pos = s_cnt[bin] + (key[k] & 0xffffu);
-        const uint32_t js = r0 + threadIdx.x + k * kBlock;
-        const uint32_t wi = fdiv(js, pl.div_p), p = js - wi * (uint32_t)pl.P;
-        const BinUnit bu = bin_unit(pl, g, w, wi);
-        const size_t si = bu.bqh * LP + (size_t)l * pl.P + p;
-        float u[3];
-        uint32_t flags;
-        int tib;
-        sample_tile<DIM>(pl, lv, static_cast<const TC*>(bf.loc) + si * DIM, u, &flags, &tib);
         uint32_t* rec = s_rec + pos * RW;
-        rec[0] = (bu.q * (uint32_t)pl.P + p) | flags;
-        rec[1] = __builtin_bit_cast(uint32_t, u[0]);
-        rec[2] = __builtin_bit_cast(uint32_t, u[1]);
-        if constexpr (DIM == 3) rec[3] = __builtin_bit_cast(uint32_t, u[2]);
-        rec[RW - 1] = __builtin_bit_cast(uint32_t, (float)static_cast<const TC*>(bf.attn)[si]);
+#pragma unroll
+        for (int i = 0; i < RW; ++i) rec[i] = rw[k][i];
         s_key[pos] = bin;
       }
       __syncthreads();
