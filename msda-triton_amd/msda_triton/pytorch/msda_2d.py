@@ -33,3 +33,7 @@ def msda2d_pytorch(
 
 
 __all__ = ["msda2d_pytorch"]
+
+
+# the attention module, at the reference's import path (pytorch/msda_2d.py)
+from msda_triton.modules import MSDA2D  # noqa: E402

@@ -33,3 +33,7 @@ def msda3d_pytorch(
 
 
 __all__ = ["msda3d_pytorch"]
+
+
+# the attention module, at the reference's import path (pytorch/msda_3d.py)
+from msda_triton.modules import MSDA3D  # noqa: E402

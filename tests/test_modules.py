@@ -1,0 +1,129 @@
+"""MSDA2D / MSDA3D modules (msda_triton.modules, re-exported from msda_triton.pytorch).
+
+CPU: init_weights patterns against what their geometry fixes (2D: the eight compass
+directions scaled to the unit square, times p + 1; 3D: points on circles of radius
+0.5 * 0.02 * (p + 1) in (x, y) with z = 2 * radius * sin(2 * angle)), argument checks, and
+that the module refuses CPU tensors (no CPU fallback).
+GPU: forward and parameter gradients equal those of the same module whose sampling step
+is the oracle (oracle/torch_ref), run on the CPU in fp32, within 1e-4 normwise; exercised
+with query and head chunking, padding mask, positional encoding, sequence-first layout and
+checkpointing.
+"""
+
+from __future__ import annotations
+
+import copy
+import math
+
+import pytest
+import torch
+
+from msda_triton.pytorch import MSDA2D, MSDA3D
+from oracle import torch_ref
+from tests._util import max_rel
+
+
+def test_import_paths():
+    from msda_triton.pytorch.msda_2d import MSDA2D as A
+    from msda_triton.pytorch.msda_3d import MSDA3D as B
+    assert A is MSDA2D and B is MSDA3D
+
+
+def test_init_weights_2d_pattern():
+    m = MSDA2D(64, num_heads=8, num_levels=3, num_points=4)
+    m.init_weights()
+    b = m.sampling_offsets.bias.detach().view(8, 3, 4, 2)
+    s = 1.0 / math.sqrt(2.0)
+    unit = torch.tensor([[1, 0], [s, s], [0, 1], [-s, s], [-1, 0], [-s, -s], [0, -1], [s, -s]])
+    unit = unit / unit.abs().amax(-1, keepdim=True)       # corners of the unit square
+    for p in range(4):
+        for lvl in range(3):
+            assert torch.allclose(b[:, lvl, p], unit * (p + 1), atol=1e-6)
+    assert torch.all(m.sampling_offsets.weight == 0) and torch.all(m.attention_weights.weight == 0)
+    assert torch.all(m.attention_weights.bias == 0) and torch.all(m.value_proj.bias == 0)
+    lim = math.sqrt(6.0 / (64 + 64))                     # Xavier-uniform bound
+    assert m.value_proj.weight.abs().max() <= lim and m.output_proj.weight.abs().max() <= lim
+
+
+def test_init_weights_3d_pattern():
+    H, L, P = 4, 2, 3
+    m = MSDA3D(32, num_heads=H, num_levels=L, num_points=P)
+    m.init_weights()
+    b = m.sampling_offsets.bias.detach().double().view(H, L, P, 3)
+    assert torch.equal(b[:, 0], b[:, 1])
+    for h in range(H):
+        for p in range(P):
+            r = 0.02 * (p + 1)
+            x, y, z = b[h, 0, p]
+            assert abs(math.hypot(x, y) - 0.5 * r) < 1e-7
+            a = math.atan2(y, x) % (2 * math.pi)
+            assert abs(a - 2 * math.pi * (h * P + p) / (H * P)) < 1e-5
+            assert abs(z - 2 * r * math.sin(2 * a)) < 1e-7
+
+
+def test_argument_checks():
+    with pytest.raises(ValueError, match="divisible"):
+        MSDA2D(30, num_heads=8, num_levels=1, num_points=1)
+    m = MSDA2D(16, num_heads=2, num_levels=1, num_points=2, batch_first=True)
+    q = torch.randn(1, 5, 16)
+    shapes = torch.tensor([[2, 3]])
+    with pytest.raises(ValueError, match="Last dim of reference_points must be 2"):
+        m(q, value=torch.randn(1, 6, 16), reference_points=torch.rand(1, 5, 1, 3),
+          spatial_shapes=shapes)
+    with pytest.raises(AssertionError):
+        m(q, value=torch.randn(1, 7, 16), reference_points=torch.rand(1, 5, 1, 2),
+          spatial_shapes=shapes)
+
+
+def test_cpu_tensors_are_refused():
+    m = MSDA2D(16, num_heads=2, num_levels=1, num_points=2, batch_first=True)
+    with pytest.raises(ValueError, match="CUDA"):
+        m(torch.randn(1, 5, 16), value=torch.randn(1, 6, 16),
+          reference_points=torch.rand(1, 5, 1, 2), spatial_shapes=torch.tensor([[2, 3]]))
+
+
+def _oracle_module(m):
+    """A CPU copy of module m whose sampling step is the oracle."""
+    r = copy.deepcopy(m).cpu()
+    r._msda = lambda v, s, lo, a: torch_ref.msda_ref(v, s, lo, a, r.clamp_grid, r.clamp_eps)
+    return r
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dim", [2, 3])
+def test_module_matches_oracle_module(dim):
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    torch.manual_seed(0)
+    cls = MSDA2D if dim == 2 else MSDA3D
+    shapes = torch.tensor([[12, 10], [6, 5]] if dim == 2 else [[4, 6, 5], [2, 3, 3]])
+    nv = int(shapes.prod(-1).sum())
+    E, H, nq, bs = 64, 4, 37, 2
+    m = cls(E, num_heads=H, num_levels=2, num_points=3, dropout=0.0, query_chunk_size=16,
+            head_chunk_size=3, use_checkpoint=True)
+    m.init_weights()
+    with torch.no_grad():  # non-trivial offsets and weights
+        m.sampling_offsets.weight.normal_(0, 0.05)
+        m.attention_weights.weight.normal_(0, 0.2)
+    m.train()
+    ref = _oracle_module(m)
+    print(f"module parity dim={dim}", flush=True)
+    g = torch.Generator().manual_seed(1)
+    query = torch.randn(nq, bs, E, generator=g)          # sequence-first (batch_first=False)
+    value = torch.randn(nv, bs, E, generator=g)
+    pos = torch.randn(nq, bs, E, generator=g)
+    refp = torch.rand(bs, nq, 2, dim, generator=g)
+    mask = torch.rand(bs, nv, generator=g) < 0.1
+    grad = torch.randn(nq, bs, E, generator=g)
+    dev = torch.device("cuda")
+    m = m.to(dev)
+    out = m(query.to(dev), value=value.to(dev), query_pos=pos.to(dev), key_padding_mask=mask.to(dev),
+            reference_points=refp.to(dev), spatial_shapes=shapes)
+    out.backward(grad.to(dev))
+    out_r = ref(query, value=value, query_pos=pos, key_padding_mask=mask, reference_points=refp,
+                spatial_shapes=shapes)
+    out_r.backward(grad)
+    assert out.shape == (nq, bs, E)
+    assert max_rel(out.detach().cpu(), out_r.detach()) <= 1e-4
+    for (name, p), (_, pr) in zip(m.named_parameters(), ref.named_parameters()):
+        assert max_rel(p.grad.cpu(), pr.grad) <= 1e-4, name
