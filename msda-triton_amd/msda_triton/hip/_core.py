@@ -9,7 +9,9 @@ libmsda_hip.so (csrc/msda_kernels.hip) and are reached through include/msda.h.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
+import weakref
 from collections import OrderedDict
 
 import torch
@@ -25,6 +27,10 @@ _INT32_MAX = 2**31 - 1
 # Device copies of CPU-resident level tables, keyed by (dim, shapes, device).
 _LEVEL_CACHE: OrderedDict = OrderedDict()
 _LEVEL_CACHE_MAX = 64
+# Level tables derived from GPU-resident shape tensors, keyed by id(tensor) and valid while
+# that tensor is alive and unmodified (same version counter): a loop over one shapes
+# tensor pays the device-side conversion once.
+_GPU_LEVEL_CACHE: OrderedDict = OrderedDict()
 
 
 def validate_inputs(name: str, dim: int, value: torch.Tensor, value_spatial_shapes: torch.Tensor,
@@ -85,7 +91,18 @@ class Levels:
         self._host = host
         self._event = event
 
+    def start_host_copy(self) -> None:
+        """Begin the asynchronous device-to-host copy of the shapes (GPU-resident shapes
+        only; the backward plans from the host copy)."""
+        if self._host is None:
+            host = torch.empty(self.spatial.shape, dtype=torch.int32, pin_memory=True)
+            host.copy_(self.spatial, non_blocking=True)
+            event = torch.cuda.Event()
+            event.record(torch.cuda.current_stream(self.spatial.device))
+            self._host, self._event = host, event
+
     def host(self) -> torch.Tensor:
+        self.start_host_copy()
         if self._event is not None:
             self._event.synchronize()
             self._event = None
@@ -98,7 +115,8 @@ def prepare_levels(dim: int, value: torch.Tensor, value_spatial_shapes: torch.Te
     CPU-resident shapes are checked against K and the int32 range (as in
     _prepare_spatial_2d, triton/msda_2d.py:53-74) and their device copy is cached.
     GPU-resident shapes are converted on the device without a host sync and without the
-    K check (triton/msda_2d.py:76-82); their host copy is started asynchronously.
+    K check (triton/msda_2d.py:76-82), cached for the live, unmodified tensor; their host
+    copy (needed by the backward only) starts with Levels.start_host_copy().
     """
     device = value.device
     if value_spatial_shapes.device.type == "cpu":
@@ -133,16 +151,29 @@ def prepare_levels(dim: int, value: torch.Tensor, value_spatial_shapes: torch.Te
         if len(_LEVEL_CACHE) > _LEVEL_CACHE_MAX:
             _LEVEL_CACHE.popitem(last=False)
         return levels
+    key = id(value_spatial_shapes)
+    hit = _GPU_LEVEL_CACHE.get(key)
+    if hit is not None:
+        ref, version, hdim, hdev, levels = hit
+        if (ref() is value_spatial_shapes and version == value_spatial_shapes._version
+                and hdim == dim and hdev == device):
+            _GPU_LEVEL_CACHE.move_to_end(key)
+            return levels
+        del _GPU_LEVEL_CACHE[key]
     spatial_i32 = value_spatial_shapes.to(device=device, dtype=torch.int32).contiguous()
     sizes = spatial_i32.to(torch.int64).prod(dim=1)
     starts = torch.zeros_like(sizes)
     if sizes.numel() > 1:
         starts[1:] = torch.cumsum(sizes[:-1], dim=0)
-    host = torch.empty(spatial_i32.shape, dtype=torch.int32, pin_memory=True)
-    host.copy_(spatial_i32, non_blocking=True)
-    event = torch.cuda.Event()
-    event.record(torch.cuda.current_stream(device))
-    return Levels(spatial_i32, starts.to(torch.int32), host, event)
+    levels = Levels(spatial_i32, starts.to(torch.int32), None)
+    try:
+        ref = weakref.ref(value_spatial_shapes)
+    except TypeError:
+        return levels
+    _GPU_LEVEL_CACHE[key] = (ref, value_spatial_shapes._version, dim, device, levels)
+    if len(_GPU_LEVEL_CACHE) > _LEVEL_CACHE_MAX:
+        _GPU_LEVEL_CACHE.popitem(last=False)
+    return levels
 
 
 def coord_dtype(value: torch.Tensor, loc: torch.Tensor, attn: torch.Tensor) -> torch.dtype:
@@ -180,6 +211,13 @@ def _aligned(t: torch.Tensor) -> torch.Tensor:
     return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
+def _on_device(device: torch.device):
+    """Context that makes device current, or nothing if it already is."""
+    if device.index is None or device.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(device)
+
+
 def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
@@ -200,7 +238,7 @@ def forward(dim: int, value: torch.Tensor, levels: Levels, loc: torch.Tensor, at
     # optional workspace: a head-major copy of value for large, line-sharing value slices
     ws_bytes = int(lib.msda_fwd_workspace_bytes(ctypes.byref(desc)))
     ws = torch.empty(ws_bytes, device=value.device, dtype=torch.uint8) if ws_bytes else None
-    with torch.cuda.device(value.device):
+    with _on_device(value.device):
         rc = lib.msda_fwd(ctypes.byref(desc), value_c.data_ptr(), levels.spatial.data_ptr(),
                           levels.starts.data_ptr(), loc_c.data_ptr(), attn_c.data_ptr(),
                           out.data_ptr(), ws.data_ptr() if ws is not None else None, ws_bytes,
@@ -225,7 +263,7 @@ def backward(dim: int, grad_output: torch.Tensor, value_c: torch.Tensor, levels:
     if ws_bytes == 0 and _lib.last_error():
         _lib.check(_lib.MSDA_ERR_INVALID, "msda_bwd_workspace_bytes")
     ws = torch.empty(max(ws_bytes, 1), device=value_c.device, dtype=torch.uint8)
-    with torch.cuda.device(value_c.device):
+    with _on_device(value_c.device):
         rc = lib.msda_bwd(ctypes.byref(desc), host.data_ptr(), value_c.data_ptr(),
                           loc_c.data_ptr(), attn_c.data_ptr(), grad_out.data_ptr(),
                           grad_value.data_ptr(), grad_loc.data_ptr(), grad_attn.data_ptr(),
@@ -239,6 +277,7 @@ def fn_forward(ctx, name: str, dim: int, value, value_spatial_shapes, sampling_l
     """Body of MSDA2DFn.forward / MSDA3DFn.forward (reference triton/msda_2d.py:749-775)."""
     validate_inputs(name, dim, value, value_spatial_shapes, sampling_locations, attention_weights)
     levels = prepare_levels(dim, value, value_spatial_shapes)
+    levels.start_host_copy()  # the backward plans from it; overlap the copy with the forward
     out, value_c, loc_c, attn_c = forward(dim, value, levels, sampling_locations,
                                           attention_weights, clamp_grid, clamp_eps)
     ctx.save_for_backward(value_c, loc_c, attn_c)

@@ -225,6 +225,19 @@ class ParitySuite:
                      *self.gpu(loc, attn)).cpu()
         assert torch.equal(a, b)
 
+    def test_gpu_resident_shapes_modified_in_place(self) -> None:
+        """The level tables cached for a device shapes tensor follow in-place edits."""
+        ss = [(32, 32), (16, 16)] if self.dim == 2 else [(4, 5, 5), (2, 3, 3)]
+        value, shapes, loc, attn = self.inputs(batch_size=1, spatial_shapes=ss)
+        shapes_dev = shapes.to(self.device, torch.int32)
+        a = self.fwd(*self.gpu(value), shapes_dev, *self.gpu(loc, attn)).cpu()
+        assert max_rel(a, torch_ref.msda_ref(value, shapes, loc, attn)) <= FWD_TOL_F32
+        new = torch.tensor([[16, 64], [16, 16]] if self.dim == 2 else [[5, 4, 5], [2, 3, 3]])
+        shapes_dev.copy_(new)  # same K, different level geometry
+        b = self.fwd(*self.gpu(value), shapes_dev, *self.gpu(loc, attn)).cpu()
+        assert max_rel(b, torch_ref.msda_ref(value, new, loc, attn)) <= FWD_TOL_F32
+        assert not torch.equal(a, b)
+
     def test_non_contiguous_inputs(self) -> None:
         value, shapes, loc, attn = self.inputs(batch_size=2, num_queries=30)
         ref = torch_ref.msda_ref(value, shapes, loc, attn)
