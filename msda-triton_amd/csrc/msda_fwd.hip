@@ -164,7 +164,17 @@ __device__ inline void fetch_level(const Sample<DIM> (&sm)[SB], const FwdLevel& 
 //
 // STAGED: levels flagged kLvlStaged are read from s_rows; zoff is the lane's offset in the
 // all-zero row there.
-template <int DIM, typename EV, typename EC, int VEC, int PT, bool STAGED>
+//
+// SHARE (PT > 0, units of 4, 8, ... lanes, all active): lane q of each quad computes the
+// geometry of sample q % SB of the batch only (corner weights times attn, and corner row
+// offsets without its own channel offset); the quad's lanes exchange those with DPP
+// quad broadcasts instead of each lane recomputing every sample of the batch.
+template <int K>
+__device__ inline uint32_t quad_bcast(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, K * 0x55, 0xF, 0xF, true);
+}
+
+template <int DIM, typename EV, typename EC, int VEC, int PT, bool STAGED, bool SHARE = false>
 __device__ inline void unit_forward(const Params& p, const FwdLevel* s_lvl, const char* s_rows,
                                     uint32_t zoff, uint32_t b, uint32_t h, uint32_t bqh,
                                     uint32_t lane, float (&acc)[VEC]) {
@@ -202,6 +212,110 @@ __device__ inline void unit_forward(const Params& p, const FwdLevel* s_lvl, cons
       }
     }
     const int gbase = (int)(__lane_id() & ~((1u << p.lpu_log2) - 1u));  // first lane of the group
+    if constexpr (SHARE) {
+      const int ks = (int)(lane & 3u) % SB;  // the batch sample this lane computes
+      const uint32_t vbase0 = vbase - lane_off;
+      const uint32_t zoff0 = zoff - lane_off;
+#pragma unroll 1
+      for (int bi = 0; bi < nbatch; ++bi) {
+        const int l = bi / BPL;
+        const FwdLevel lv = s_lvl[l];
+        const int sl = bi / nv;
+        const int src = (gbase + (bi - sl * nv)) << 2;
+        CoordBlock<EC, SB * DIM> lb;
+        CoordBlock<EC, SB> ab;
+#pragma unroll
+        for (int w = 0; w < LW; ++w) {
+          uint32_t x = hl[0].d[w];
+#pragma unroll
+          for (int k = 1; k < kFwdCoordSlots<DIM>; ++k) x = sl == k ? hl[k].d[w] : x;
+          lb.d[w] = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)x);
+        }
+#pragma unroll
+        for (int w = 0; w < AW; ++w) {
+          uint32_t x = ha[0].d[w];
+#pragma unroll
+          for (int k = 1; k < kFwdCoordSlots<DIM>; ++k) x = sl == k ? ha[k].d[w] : x;
+          ab.d[w] = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)x);
+        }
+        // this lane's sample: coordinates and weight picked from the batch block
+        float xyz[DIM], a = block_elem(ab, 0);
+#pragma unroll
+        for (int d = 0; d < DIM; ++d) xyz[d] = block_elem(lb, d);
+#pragma unroll
+        for (int k = 1; k < SB; ++k) {
+          a = ks == k ? block_elem(ab, k) : a;
+#pragma unroll
+          for (int d = 0; d < DIM; ++d) xyz[d] = ks == k ? block_elem(lb, k * DIM + d) : xyz[d];
+        }
+        Sample<DIM> sm;
+        sm.ax = make_axis(xyz[0], (float)lv.W, lv.W, p.clamp, p.lo_g, p.hi_g);
+        sm.ay = make_axis(xyz[1], (float)lv.H, lv.H, p.clamp, p.lo_g, p.hi_g);
+        if constexpr (DIM == 3) sm.az = make_axis(xyz[2], (float)lv.D, lv.D, p.clamp, p.lo_g, p.hi_g);
+        const bool lds = STAGED && (lv.flags & kLvlStaged);
+        int32_t o0;
+        if (lv.flags & kLvlMul24) {
+          o0 = __mul24(sm.ay.i0, lv.sy) + __mul24(sm.ax.i0, lv.sx);
+          if constexpr (DIM == 3) o0 += __mul24(sm.az.i0, lv.sz);
+        } else {
+          o0 = sm.ay.i0 * lv.sy + sm.ax.i0 * lv.sx;
+          if constexpr (DIM == 3) o0 += sm.az.i0 * lv.sz;
+        }
+        const uint32_t obase = (lds ? 0u : vbase0) + lv.base + (uint32_t)o0;
+        const uint32_t obad = lds ? zoff0 : kOobOffset;
+        uint32_t mo[NC], mw[NC];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const uint32_t dr = ((c & 1) ? (uint32_t)lv.sx : 0u) + ((c & 2) ? (uint32_t)lv.sy : 0u) +
+                              ((DIM == 3 && (c & 4)) ? (uint32_t)lv.sz : 0u);
+          mo[c] = corner_valid<DIM>(c, sm) ? obase + dr : obad;
+          mw[c] = as_u32(corner_weight<DIM>(c, sm) * a);
+        }
+        // every sample of the batch from the quad lane that computed it
+        uint32_t off[SB][NC];
+        float cw[SB][NC];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          off[0][c] = quad_bcast<0>(mo[c]) + lane_off;
+          cw[0][c] = as_float(quad_bcast<0>(mw[c]));
+          if constexpr (SB > 1) {
+            off[1][c] = quad_bcast<1>(mo[c]) + lane_off;
+            cw[1][c] = as_float(quad_bcast<1>(mw[c]));
+          }
+          if constexpr (SB > 2) {
+            off[2][c] = quad_bcast<2>(mo[c]) + lane_off;
+            cw[2][c] = as_float(quad_bcast<2>(mw[c]));
+          }
+          if constexpr (SB > 3) {
+            off[3][c] = quad_bcast<3>(mo[c]) + lane_off;
+            cw[3][c] = as_float(quad_bcast<3>(mw[c]));
+          }
+        }
+        RawVec<VB> raw[SB][NC];
+        if (lds) {
+#pragma unroll
+          for (int k = 0; k < SB; ++k)
+#pragma unroll
+            for (int c = 0; c < NC; ++c) raw[k][c] = *reinterpret_cast<const RawVec<VB>*>(s_rows + off[k][c]);
+        } else {
+#pragma unroll
+          for (int k = 0; k < SB; ++k)
+#pragma unroll
+            for (int c = 0; c < NC; ++c) raw[k][c] = buf_load<VB>(rv, off[k][c]);
+        }
+#pragma unroll
+        for (int k = 0; k < SB; ++k) {
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            float v[VEC];
+            widen<EV, VEC>(raw[k][c], v);
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) acc[i] = __builtin_fmaf(cw[k][c], v[i], acc[i]);
+          }
+        }
+      }
+      return;
+    }
 #pragma unroll 1
     for (int bi = 0; bi < nbatch; ++bi) {
       const int l = bi / BPL;
@@ -308,7 +422,7 @@ __global__ __launch_bounds__(kBlock) void msda_fwd_kernel(const Params p) {
 
 // Same result as msda_fwd_kernel; the smallest levels of the workgroup's (batch, head)
 // value slice are read from LDS.
-template <int DIM, typename EV, typename EC, int VEC, int PT>
+template <int DIM, typename EV, typename EC, int VEC, int PT, bool SHARE>
 __global__ __launch_bounds__(kFwdStageThreads) void msda_fwd_staged_kernel(const Params p) {
   constexpr int NT = kFwdStageThreads;
   constexpr int VB = VEC * EV::kBytes;
@@ -405,7 +519,7 @@ __global__ __launch_bounds__(kFwdStageThreads) void msda_fwd_staged_kernel(const
     if (q >= q1) break;
     const uint32_t bqh = (b * p.Q + q) * (uint32_t)p.H + h;
     float acc[VEC];
-    unit_forward<DIM, EV, EC, VEC, PT, true>(p, s_lvl, s_rows, zrow + lane * VB, b, h, bqh, lane, acc);
+    unit_forward<DIM, EV, EC, VEC, PT, true, SHARE>(p, s_lvl, s_rows, zrow + lane * VB, b, h, bqh, lane, acc);
     typename EV::T* outp = static_cast<typename EV::T*>(p.out) + (size_t)bqh * p.C + lane * VEC;
     store_vec<EV, VEC>(outp, acc);
   }
@@ -433,12 +547,18 @@ static hipError_t launch_fwd(const Params& p, hipStream_t s) {
 template <int DIM, typename EV, typename EC, int VEC>
 static hipError_t launch_fwd_staged(const Params& p, hipStream_t s) {
   const dim3 g(p.nblocks), t(kFwdStageThreads);
-  if (pt_path<DIM, 4>(p))
-    hipLaunchKernelGGL((msda_fwd_staged_kernel<DIM, EV, EC, VEC, 4>), g, t, p.stage_bytes, s, p);
+  // quad-shared geometry when every lane of a unit's 4-lane quads is active
+  const bool share = p.lpu_log2 >= 2 && p.nvec == (1 << p.lpu_log2);
+  if (pt_path<DIM, 4>(p) && share)
+    hipLaunchKernelGGL((msda_fwd_staged_kernel<DIM, EV, EC, VEC, 4, true>), g, t, p.stage_bytes, s, p);
+  else if (pt_path<DIM, 8>(p) && share)
+    hipLaunchKernelGGL((msda_fwd_staged_kernel<DIM, EV, EC, VEC, 8, true>), g, t, p.stage_bytes, s, p);
+  else if (pt_path<DIM, 4>(p))
+    hipLaunchKernelGGL((msda_fwd_staged_kernel<DIM, EV, EC, VEC, 4, false>), g, t, p.stage_bytes, s, p);
   else if (pt_path<DIM, 8>(p))
-    hipLaunchKernelGGL((msda_fwd_staged_kernel<DIM, EV, EC, VEC, 8>), g, t, p.stage_bytes, s, p);
+    hipLaunchKernelGGL((msda_fwd_staged_kernel<DIM, EV, EC, VEC, 8, false>), g, t, p.stage_bytes, s, p);
   else
-    hipLaunchKernelGGL((msda_fwd_staged_kernel<DIM, EV, EC, VEC, 0>), g, t, p.stage_bytes, s, p);
+    hipLaunchKernelGGL((msda_fwd_staged_kernel<DIM, EV, EC, VEC, 0, false>), g, t, p.stage_bytes, s, p);
   return hipGetLastError();
 }
 
