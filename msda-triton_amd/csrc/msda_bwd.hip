@@ -788,13 +788,36 @@ __global__ __launch_bounds__(kTileThreads, kTileWavesPerSimd) void bwd_tile_kern
 }
 
 // ------------------------------------------------------------------ 6: fold
+// o += src[j * stride] for j = 0 .. n-1, in that order; four chunks' loads are issued
+// before their additions so their latencies overlap.
+template <int VEC>
+__device__ inline void add_partials(float (&o)[VEC], const float* src, size_t stride, uint32_t n) {
+  uint32_t j = 0;
+  for (; j + 4 <= n; j += 4) {
+    float v[4][VEC];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) v[u][k] = src[(j + u) * stride + k];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) o[k] += v[u][k];
+  }
+  for (; j < n; ++j)
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) o[k] += src[j * stride + k];
+}
+
 // One workgroup per tile. Sums, for every edge cell (and every cell of a split tile), the
 // partials of the tile's own chunks and then the halo partials of the chunks of the lower
 // neighbours whose halo covers the cell, and writes the cell in the value dtype.
 template <int DIM, typename EV, int VEC>
 __global__ __launch_bounds__(kBlock) void bwd_fold_kernel(const BwdPlan pl, const BwdBuffers bf) {
   typedef typename EV::T TV;
-  const uint32_t t = blockIdx.x;
+  // tiles in contiguous ranges per XCD, like the tile kernel's chunks, so most partials
+  // are read from the L2 that wrote them
+  const uint32_t t = xcd_logical_block(blockIdx.x, gridDim.x);
   const uint32_t off = bf.chunk_off[t];
   const uint32_t nch = bf.chunk_off[t + 1] - off;
   const TileCoord tc = decode_tile(pl, t);
@@ -812,11 +835,8 @@ __global__ __launch_bounds__(kBlock) void bwd_fold_kernel(const BwdPlan pl, cons
 #pragma unroll
     for (int k = 0; k < VEC; ++k) o[k] = 0.0f;
     const int rc = (lz * pl.RY + ly) * pl.RX + lx;
-    for (uint32_t j = 0; j < nch; ++j) {
-      const float* src = bf.scratch + ((size_t)(off + j) * pl.rcells + rc) * pl.C + ch * VEC;
-#pragma unroll
-      for (int k = 0; k < VEC; ++k) o[k] += src[k];
-    }
+    add_partials<VEC>(o, bf.scratch + ((size_t)off * pl.rcells + rc) * pl.C + ch * VEC,
+                      (size_t)pl.rcells * pl.C, nch);
     for (int nb = 1; nb < (1 << DIM); ++nb) {
       const int dx = nb & 1, dy = (nb >> 1) & 1, dz = (nb >> 2) & 1;
       if ((dx && (lx != 0 || tc.tx == 0)) || (dy && (ly != 0 || tc.ty == 0)) ||
@@ -826,11 +846,8 @@ __global__ __launch_bounds__(kBlock) void bwd_fold_kernel(const BwdPlan pl, cons
       const uint32_t tn = tc.g * (uint32_t)pl.bins + (((uint32_t)tibn << pl.hg_log2) | tc.hsub);
       const int rn = ((lz + dz * pl.TZ) * pl.RY + (ly + dy * pl.TY)) * pl.RX + (lx + dx * pl.TX);
       const uint32_t noff = bf.chunk_off[tn], nn = bf.chunk_off[tn + 1] - noff;
-      for (uint32_t j = 0; j < nn; ++j) {
-        const float* src = bf.scratch + ((size_t)(noff + j) * pl.rcells + rn) * pl.C + ch * VEC;
-#pragma unroll
-        for (int k = 0; k < VEC; ++k) o[k] += src[k];
-      }
+      add_partials<VEC>(o, bf.scratch + ((size_t)noff * pl.rcells + rn) * pl.C + ch * VEC,
+                        (size_t)pl.rcells * pl.C, nn);
     }
     const uint32_t row = (uint32_t)lv.start + ((uint32_t)z * lv.H + y) * lv.W + x;
     store_vec<EV, VEC>(gv + (((size_t)tc.b * pl.K + row) * pl.H + tc.h) * pl.C + ch * VEC, o);
