@@ -440,8 +440,8 @@ __global__ __launch_bounds__(kBlock) void bwd_fill_kernel(const BwdPlan pl, cons
   uint32_t* s_base = s_fill;               // [bins] next global record of each bin
   uint32_t* s_cnt = s_base + pl.bins;      // [bins] round counts -> round offsets
   uint32_t* s_rec = s_cnt + pl.bins;       // [kFillStage * RW] records sorted by bin
-  uint32_t* s_key = s_rec + kFillStage * RW;  // [kFillStage] bin of each sorted record
-  uint32_t* s_w = s_key + kFillStage;      // [kBlock / kWave]
+  uint32_t* s_dst = s_rec + kFillStage * RW;  // [kFillStage] global record index of each
+  uint32_t* s_w = s_dst + kFillStage;      // [kBlock / kWave]
   const uint32_t g = blockIdx.x / (uint32_t)pl.wgpg;
   const uint32_t w = blockIdx.x - g * (uint32_t)pl.wgpg;
   for (int i = threadIdx.x; i < pl.bins; i += kBlock)
@@ -497,18 +497,33 @@ __global__ __launch_bounds__(kBlock) void bwd_fill_kernel(const BwdPlan pl, cons
 #pragma unroll
       for (int k = 0; k < KP; ++k) {
         if (key[k] == 0xffffffffu) continue;
-        const uint32_t bin = key[k] >> 16, pos = s_cnt[bin] + (key[k] & 0xffffu);
+        const uint32_t bin = key[k] >> 16, rank = key[k] & 0xffffu, pos = s_cnt[bin] + rank;
         uint32_t* rec = s_rec + pos * RW;
 #pragma unroll
         for (int i = 0; i < RW; ++i) rec[i] = rw[k][i];
-        s_key[pos] = bin;
+        s_dst[pos] = s_base[bin] + rank;
       }
       __syncthreads();
-      // copy out: consecutive threads write consecutive records of a bin
-      for (uint32_t i = threadIdx.x; i < carry * RW; i += kBlock) {
-        const uint32_t r = i / RW, k = i - r * RW;
-        const uint32_t bin = s_key[r];
-        bf.records[(size_t)(s_base[bin] + (r - s_cnt[bin])) * RW + k] = s_rec[i];
+      // copy out: consecutive threads write consecutive records of a bin; four words per
+      // thread and step, so their LDS reads overlap
+      {
+        const uint32_t nw = carry * RW;
+        for (uint32_t i0 = threadIdx.x; i0 < nw; i0 += 4 * kBlock) {
+          uint32_t v[4], d[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const uint32_t i = i0 + (uint32_t)u * kBlock;
+            d[u] = 0xffffffffu;
+            if (i < nw) {
+              const uint32_t r = i / RW, k = i - r * RW;
+              v[u] = s_rec[i];
+              d[u] = s_dst[r] * RW + k;
+            }
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            if (d[u] != 0xffffffffu) bf.records[d[u]] = v[u];
+        }
       }
       __syncthreads();
       // advance the bins' global positions by the round's counts
