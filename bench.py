@@ -38,8 +38,8 @@ import torch  # noqa: E402
 METRIC = "MSDA fwd & fwd+bwd ms + achieved HBM GB/s, 2D encoder & 3D 4-level, bf16"
 HBM_PEAK_GBPS = 8000.0
 # kernels behind the roofline objects (the C2 bf16 launch: 2D, bf16 value and coordinates,
-# 8 channels per lane, 4 points per coordinate block)
-FWD_KERNEL = "msda::msda_fwd_staged_kernel<2, msda::BF16, msda::BF16, 8, 4>"
+# 8 channels per lane, 4 points per coordinate block, quad-shared geometry)
+FWD_KERNEL = "msda::msda_fwd_staged_kernel<2, msda::BF16, msda::BF16, 8, 4, true>"
 BWD_KERNELS = ("msda_bwd entry: bwd_grad_kernel, bwd_colscan_kernel, bwd_plan_kernel, "
                "bwd_fill_kernel, bwd_tile_kernel, bwd_fold_kernel and workspace clears")
 
@@ -283,6 +283,15 @@ def main():
     main_cfg, also_cfg = CONFIGS["c2"], CONFIGS["c5"]
     r = measure_case(main_cfg, device, args.steps, args.warmup)
     r5 = measure_case(also_cfg, device, args.steps, args.warmup)
+    # the other BASELINE.json configurations: C2 in fp32, C4 (3D 2-level) in fp32 and bf16,
+    # and C3 (decoder cross-attention, forward only: host and launch latency bound)
+    extra = {}
+    for key, name, dt in (("c2_fp32", "c2", "fp32"), ("c4_fp32", "c4", "fp32"), ("c4_bf16", "c4", "bf16")):
+        extra[key] = measure_case(dict(CONFIGS[name], dtype=dt), device, args.steps, args.warmup)
+    c3 = GpuCase(CONFIGS["c3"], device)
+    import msda_triton
+    c3_args = (c3.value, c3.shapes, c3.loc, c3.attn)
+    c3_fwd_ms = time_events(lambda: msda_triton.msda2d_fwd(*c3_args), max(args.steps, 20), args.warmup)
 
     # roofline: the forward kernel, which is one launch per msda2d_fwd call (the kernel the
     # bf16 forward target is stated on); the backward entry (sample-gradient, record fill,
@@ -327,7 +336,10 @@ def main():
                    "B": 2, "H": 8, "C": 32, "levels": main_cfg["shapes"], "K": num_keys(main_cfg),
                    "Q": main_cfg["Q"], "P": 4, "clamp_grid": True, "clamp_eps": 1e-4},
         "c2_bf16": summary(r),
-        "also": {"c5_bf16_3d_4level": summary(r5)},
+        "also": {"c5_bf16_3d_4level": summary(r5),
+                 **{k: summary(v) for k, v in extra.items()},
+                 "c3_bf16_decoder": {"fwd_ms": round(c3_fwd_ms, 5),
+                                     "note": "msda2d_fwd through the Python API (host time included)"}},
         "roofline": roofline,
         "roofline_bwd": roofline_bwd,
         "cpu_baseline": cpu,
