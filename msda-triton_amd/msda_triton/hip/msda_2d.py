@@ -11,13 +11,12 @@ from __future__ import annotations
 
 import torch
 
-from . import _core
+from . import _core, ops
 
 _NAME = "MSDA2D"
 _DIM = 2
 
 
-@torch.compiler.disable
 def msda2d_fwd(
     value: torch.Tensor,
     value_spatial_shapes: torch.Tensor,
@@ -32,6 +31,10 @@ def msda2d_fwd(
         ValueError: inputs not on the GPU, or shape mismatch.
         NotImplementedError: value dtype other than fp32, fp16, bf16.
     """
+    if torch.compiler.is_compiling():  # an opaque custom op instead of a graph break
+        with torch.no_grad():
+            return ops.msda_fwd(value, value_spatial_shapes, sampling_locations, attention_weights,
+                                _DIM, clamp_grid, clamp_eps)
     return _core.run_fwd(_NAME, _DIM, value, value_spatial_shapes, sampling_locations,
                          attention_weights, clamp_grid, clamp_eps)
 
@@ -70,6 +73,9 @@ def msda2d(
     """
     if not value.is_cuda:
         raise ValueError(f"{_NAME} HIP kernel requires CUDA tensors. Got CPU tensors instead.")
+    if torch.compiler.is_compiling():  # differentiable custom op (msda_triton::msda_fwd)
+        return ops.msda_fwd(value, value_spatial_shapes, sampling_locations, attention_weights,
+                            _DIM, clamp_grid, clamp_eps)
     return MSDA2DFn.apply(value, value_spatial_shapes, sampling_locations, attention_weights,
                           clamp_grid, clamp_eps)
 
