@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define MSDA_ABI_VERSION 2
+#define MSDA_ABI_VERSION 3
 
 typedef enum msda_dtype {
   MSDA_F32 = 0,
@@ -150,6 +150,70 @@ int msda_bwd(const msda_desc* desc,
              void* workspace,
              size_t workspace_bytes,
              void* stream);
+
+/*
+ * Fused producer variant of msda_fwd: instead of sampling_locations and attention_weights
+ * it reads what the attention modules produce before them, and forms both in fp32 inside
+ * the kernel:
+ *   loc[b,q,h,l,p,d] = reference_points[b,q,l,d] + sampling_offsets[b,q,h,l,p,d] / size_l[d]
+ *                      with size_l = (W_l, H_l) for dim 2 and (W_l, H_l, D_l) for dim 3
+ *   attn[b,q,h,l,p]  = softmax over (l, p) of attention_logits[b,q,h,:]
+ *   reference_points  (B, Q, L, dim)        float32, contiguous, in [0, 1] per level
+ *   sampling_offsets  (B, Q, H, L, P, dim)  coord_dtype, contiguous, in pixels of level l
+ *   attention_logits  (B, Q, H, L, P)       coord_dtype, contiguous
+ * Other arguments, the workspace and the output are as for msda_fwd. The locations and
+ * weights never reach memory.
+ *
+ * Replaces the location and weight formation of the reference modules followed by the
+ * forward launch: src/msda_triton/pytorch/msda_2d.py:303-339 (offset normaliser, softmax
+ * over L*P, reference + offset / normaliser) and src/msda_triton/pytorch/msda_3d.py:314-350,
+ * then src/msda_triton/triton/msda_2d.py:606-651 / msda_3d.py:749-794.
+ */
+int msda_fwd_fused(const msda_desc* desc,
+                   const void* value,
+                   const int32_t* spatial_shapes,
+                   const int32_t* level_start,
+                   const float* reference_points,
+                   const void* sampling_offsets,
+                   const void* attention_logits,
+                   void* output,
+                   void* workspace,
+                   size_t workspace_bytes,
+                   void* stream);
+
+/*
+ * Bytes of device workspace msda_bwd_fused needs (0 when there is nothing to sample): fp32
+ * locations, weights and their gradients, plus the msda_bwd workspace for them.
+ */
+size_t msda_bwd_fused_workspace_bytes(const msda_desc* desc, const int32_t* host_spatial_shapes);
+
+/*
+ * Backward of msda_fwd_fused with respect to value, reference_points, sampling_offsets and
+ * attention_logits:
+ *   grad_sampling_offsets = grad_loc / size_l
+ *   grad_reference_points = sum over (h, p) of grad_loc                       (float32)
+ *   grad_attention_logits = attn * (grad_attn - sum over (l, p) of attn * grad_attn)
+ * where grad_loc and grad_attn are msda_bwd's gradients at the fp32 locations and weights
+ * the forward formed. All outputs are fully overwritten; grad_value as in msda_bwd.
+ *
+ * Replaces autograd through the same reference module lines as msda_fwd_fused plus the
+ * MSDA2DFn / MSDA3DFn backward (src/msda_triton/triton/msda_2d.py:778-853,
+ * msda_3d.py:920-996).
+ */
+int msda_bwd_fused(const msda_desc* desc,
+                   const int32_t* host_spatial_shapes,
+                   const void* value,
+                   const float* reference_points,
+                   const void* sampling_offsets,
+                   const void* attention_logits,
+                   const void* grad_output,
+                   void* grad_value,
+                   float* grad_reference_points,
+                   void* grad_sampling_offsets,
+                   void* grad_attention_logits,
+                   void* workspace,
+                   size_t workspace_bytes,
+                   void* stream);
 
 #ifdef __cplusplus
 }

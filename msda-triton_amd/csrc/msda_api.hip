@@ -397,6 +397,149 @@ void carve(char* ws, const msda::BwdSizes& z, msda::BwdBuffers* bf) {
   bf->value_h = z.value_h_bytes ? p : nullptr;
 }
 
+// Body of msda_fwd and msda_fwd_fused. fused: `loc` / `attn` are the sampling offsets and
+// attention logits and `ref` the fp32 reference points; the kernels form the locations and
+// weights themselves.
+int fwd_impl(const msda_desc* d, const void* value, const int32_t* spatial_shapes,
+             const int32_t* level_start, const void* sampling_locations,
+             const void* attention_weights, const float* ref, void* output, void* workspace,
+             size_t workspace_bytes, void* stream, bool fused) {
+  const char* name = fused ? "msda_fwd_fused" : "msda_fwd";
+  int rc = validate(d);
+  if (rc) return rc;
+  const uint64_t units = (uint64_t)d->batch * d->num_queries * d->num_heads;
+  if (units == 0) return MSDA_OK;
+  const bool has_samples = d->num_levels > 0 && d->num_points > 0;
+  if (!output || (d->num_keys > 0 && !value) ||
+      (has_samples && (!sampling_locations || !attention_weights || (fused && !ref))) ||
+      (d->num_levels > 0 && (!spatial_shapes || !level_start)))
+    return fail(MSDA_ERR_INVALID, "%s: required pointer is NULL", name);
+  const void* vptrs[2] = {value, output};
+  Layout lay;
+  if ((rc = choose_layout(d, vptrs, 2, &lay))) return rc;
+  msda::LaunchFn fn = msda::get_fwd_launcher(d->dim, d->value_dtype, d->coord_dtype, lay.vec_bytes, false, fused);
+  msda::LaunchFn fn_staged =
+      msda::get_fwd_launcher(d->dim, d->value_dtype, d->coord_dtype, lay.vec_bytes, true, fused);
+  if (!fn || !fn_staged) return fail(MSDA_ERR_DTYPE, "no forward kernel for this dtype combination");
+
+  const int64_t nb = batches_per_launch(d, lay);
+  const int sv = elem_bytes(d->value_dtype), sc = elem_bytes(d->coord_dtype);
+  const uint64_t LP = (uint64_t)d->num_levels * d->num_points;
+  const uint64_t qh = (uint64_t)d->num_queries * d->num_heads;
+  const uint64_t kv = (uint64_t)d->num_keys * d->num_heads * d->channels;
+  for (int64_t b0 = 0; b0 < d->batch; b0 += nb) {
+    const int64_t bc = (d->batch - b0) < nb ? (d->batch - b0) : nb;
+    msda::Params p{};
+    fill_params(d, lay, bc, &p);
+    p.value = static_cast<const char*>(value) + (uint64_t)b0 * kv * sv;
+    p.loc = static_cast<const char*>(sampling_locations) + (uint64_t)b0 * qh * LP * d->dim * sc;
+    p.attn = static_cast<const char*>(attention_weights) + (uint64_t)b0 * qh * LP * sc;
+    p.out = static_cast<char*>(output) + (uint64_t)b0 * qh * d->channels * sv;
+    p.shapes = spatial_shapes;
+    p.starts = level_start;
+    p.ref = fused ? ref + (uint64_t)b0 * d->num_queries * d->num_levels * d->dim : nullptr;
+    p.coords_aligned = aligned(p.loc, 16) && aligned(p.attn, 16);
+    // head-major copy of this launch's value slice when it pays and the workspace holds it
+    const uint64_t vbytes = (uint64_t)bc * kv * sv;
+    if (use_head_major(d) && workspace && workspace_bytes >= vbytes &&
+        aligned(workspace, lay.vec_bytes)) {
+      hipError_t e = msda::launch_head_major(p.value, workspace, (uint32_t)bc, (uint32_t)d->num_keys,
+                                             (uint32_t)d->num_heads, (uint32_t)(d->channels * sv),
+                                             lay.vec_bytes, static_cast<hipStream_t>(stream));
+      if (e != hipSuccess) return fail(MSDA_ERR_HIP, "%s relayout failed: %s", name, hipGetErrorString(e));
+      p.value_h = workspace;
+    }
+    // Staged kernel: one workgroup per CU, each (batch, head) slice split into query
+    // ranges; used when every workgroup gets enough queries to amortise its LDS copy.
+    const uint64_t slices = (uint64_t)bc * d->num_heads;
+    const uint64_t splits = (kCus + slices - 1) / slices;
+    const uint64_t qper = ((uint64_t)d->num_queries + splits - 1) / splits;
+    // the LDS holds at least one staged row beside the all-zero row
+    const bool staged = has_samples && qper >= msda::kFwdStageMinQueries &&
+                        (uint64_t)d->channels * sv * 2 <= msda::kFwdStageLds;
+    if (staged) {
+      p.splits = (uint32_t)splits;
+      p.qper = (uint32_t)qper;
+      p.stage_bytes = msda::kFwdStageLds;
+      p.nblocks = (uint32_t)(slices * splits);
+    }
+    hipError_t e = (staged ? fn_staged : fn)(p, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(MSDA_ERR_HIP, "%s launch failed: %s", name, hipGetErrorString(e));
+  }
+  return MSDA_OK;
+}
+
+
+// Workspace of msda_bwd_fused: fp32 loc, attn, grad_loc, grad_attn, then the workspace of
+// the inner msda_bwd over those fp32 tensors (coord dtype float32).
+struct FusedWs {
+  uint64_t loc, attn, gloc, gattn, inner, total;  // byte offsets, inner: its size
+};
+
+bool fused_ws(const msda_desc* d, const int32_t* hs, FusedWs* w) {
+  auto al = [](uint64_t b) { return (b + 255) & ~(uint64_t)255; };
+  msda_desc d32 = *d;
+  d32.coord_dtype = MSDA_F32;
+  const uint64_t samples = (uint64_t)d->batch * d->num_queries * d->num_heads * d->num_levels * d->num_points;
+  w->loc = 0;
+  w->attn = w->loc + al(samples * d->dim * 4);
+  w->gloc = w->attn + al(samples * 4);
+  w->gattn = w->gloc + al(samples * d->dim * 4);
+  const uint64_t inner_off = w->gattn + al(samples * 4);
+  BwdHostPlan hp;
+  const void* none[1] = {nullptr};
+  if (plan_bwd(&d32, hs, none, 0, &hp)) return false;
+  w->inner = hp.sz.total_bytes;
+  w->total = inner_off + al(w->inner);
+  w->inner = inner_off;  // from here on: offset of the inner workspace
+  return true;
+}
+
+// Fused-path prep / grad launches over batch ranges that keep every index 32-bit.
+int run_fused_kernels(const msda_desc* d, const int32_t* hs, msda::FusedArgs a, bool grad,
+                      hipStream_t st) {
+  Layout lay;
+  const void* none[1] = {nullptr};
+  int rc = choose_layout(d, none, 0, &lay);
+  if (rc) return rc;
+  for (int l = 0; l < d->num_levels; ++l) {
+    const int32_t* r = hs + l * d->dim;
+    // the forward kernel's reciprocals: 1.0f / (float)extent, correctly rounded on both sides
+    a.inv[l][0] = 1.0f / (float)r[d->dim - 1];                   // W
+    a.inv[l][1] = 1.0f / (float)r[d->dim - 2];                   // H
+    a.inv[l][2] = 1.0f / (d->dim == 3 ? (float)r[0] : 1.0f);     // D
+  }
+  a.H = d->num_heads;
+  a.L = d->num_levels;
+  a.P = d->num_points;
+  const int64_t nb = batches_per_launch(d, lay);
+  const int sc = elem_bytes(d->coord_dtype);
+  const uint64_t LP = (uint64_t)d->num_levels * d->num_points;
+  const uint64_t qh = (uint64_t)d->num_queries * d->num_heads;
+  const uint64_t nref = (uint64_t)d->num_queries * d->num_levels * d->dim;  // per batch
+  const uint64_t nloc = qh * LP * d->dim, natt = qh * LP;                    // per batch
+  for (int64_t b0 = 0; b0 < d->batch; b0 += nb) {
+    const int64_t bc = (d->batch - b0) < nb ? (d->batch - b0) : nb;
+    msda::FusedArgs x = a;
+    x.units = (uint32_t)(bc * qh);
+    x.bq = (uint32_t)(bc * d->num_queries);
+    x.ref = a.ref ? a.ref + b0 * nref : nullptr;
+    x.off = a.off ? static_cast<const char*>(a.off) + b0 * nloc * sc : nullptr;
+    x.logits = a.logits ? static_cast<const char*>(a.logits) + b0 * natt * sc : nullptr;
+    x.loc = a.loc + b0 * nloc;
+    x.attn = a.attn + b0 * natt;
+    x.grad_loc = a.grad_loc ? a.grad_loc + b0 * nloc : nullptr;
+    x.grad_attn = a.grad_attn ? a.grad_attn + b0 * natt : nullptr;
+    x.grad_ref = a.grad_ref ? a.grad_ref + b0 * nref : nullptr;
+    x.grad_off = a.grad_off ? static_cast<char*>(a.grad_off) + b0 * nloc * sc : nullptr;
+    x.grad_logits = a.grad_logits ? static_cast<char*>(a.grad_logits) + b0 * natt * sc : nullptr;
+    hipError_t e = msda::launch_fused(x, d->dim, d->coord_dtype, grad, st);
+    if (e != hipSuccess)
+      return fail(MSDA_ERR_HIP, "msda_bwd_fused %s launch failed: %s", grad ? "grad" : "prep",
+                  hipGetErrorString(e));
+  }
+  return MSDA_OK;
+}
 }  // namespace
 
 extern "C" {
@@ -427,67 +570,17 @@ int msda_fwd(const msda_desc* d, const void* value, const int32_t* spatial_shape
              const void* attention_weights, void* output, void* workspace,
              size_t workspace_bytes, void* stream) {
   g_err[0] = 0;
-  int rc = validate(d);
-  if (rc) return rc;
-  const uint64_t units = (uint64_t)d->batch * d->num_queries * d->num_heads;
-  if (units == 0) return MSDA_OK;
-  const bool has_samples = d->num_levels > 0 && d->num_points > 0;
-  if (!output || (d->num_keys > 0 && !value) ||
-      (has_samples && (!sampling_locations || !attention_weights)) ||
-      (d->num_levels > 0 && (!spatial_shapes || !level_start)))
-    return fail(MSDA_ERR_INVALID, "msda_fwd: required pointer is NULL");
-  const void* vptrs[2] = {value, output};
-  Layout lay;
-  if ((rc = choose_layout(d, vptrs, 2, &lay))) return rc;
-  msda::LaunchFn fn = msda::get_fwd_launcher(d->dim, d->value_dtype, d->coord_dtype, lay.vec_bytes, false);
-  msda::LaunchFn fn_staged =
-      msda::get_fwd_launcher(d->dim, d->value_dtype, d->coord_dtype, lay.vec_bytes, true);
-  if (!fn || !fn_staged) return fail(MSDA_ERR_DTYPE, "no forward kernel for this dtype combination");
+  return fwd_impl(d, value, spatial_shapes, level_start, sampling_locations, attention_weights,
+                  nullptr, output, workspace, workspace_bytes, stream, false);
+}
 
-  const int64_t nb = batches_per_launch(d, lay);
-  const int sv = elem_bytes(d->value_dtype), sc = elem_bytes(d->coord_dtype);
-  const uint64_t LP = (uint64_t)d->num_levels * d->num_points;
-  const uint64_t qh = (uint64_t)d->num_queries * d->num_heads;
-  const uint64_t kv = (uint64_t)d->num_keys * d->num_heads * d->channels;
-  for (int64_t b0 = 0; b0 < d->batch; b0 += nb) {
-    const int64_t bc = (d->batch - b0) < nb ? (d->batch - b0) : nb;
-    msda::Params p{};
-    fill_params(d, lay, bc, &p);
-    p.value = static_cast<const char*>(value) + (uint64_t)b0 * kv * sv;
-    p.loc = static_cast<const char*>(sampling_locations) + (uint64_t)b0 * qh * LP * d->dim * sc;
-    p.attn = static_cast<const char*>(attention_weights) + (uint64_t)b0 * qh * LP * sc;
-    p.out = static_cast<char*>(output) + (uint64_t)b0 * qh * d->channels * sv;
-    p.shapes = spatial_shapes;
-    p.starts = level_start;
-    p.coords_aligned = aligned(p.loc, 16) && aligned(p.attn, 16);
-    // head-major copy of this launch's value slice when it pays and the workspace holds it
-    const uint64_t vbytes = (uint64_t)bc * kv * sv;
-    if (use_head_major(d) && workspace && workspace_bytes >= vbytes &&
-        aligned(workspace, lay.vec_bytes)) {
-      hipError_t e = msda::launch_head_major(p.value, workspace, (uint32_t)bc, (uint32_t)d->num_keys,
-                                             (uint32_t)d->num_heads, (uint32_t)(d->channels * sv),
-                                             lay.vec_bytes, static_cast<hipStream_t>(stream));
-      if (e != hipSuccess) return fail(MSDA_ERR_HIP, "msda_fwd relayout failed: %s", hipGetErrorString(e));
-      p.value_h = workspace;
-    }
-    // Staged kernel: one workgroup per CU, each (batch, head) slice split into query
-    // ranges; used when every workgroup gets enough queries to amortise its LDS copy.
-    const uint64_t slices = (uint64_t)bc * d->num_heads;
-    const uint64_t splits = (kCus + slices - 1) / slices;
-    const uint64_t qper = ((uint64_t)d->num_queries + splits - 1) / splits;
-    // the LDS holds at least one staged row beside the all-zero row
-    const bool staged = has_samples && qper >= msda::kFwdStageMinQueries &&
-                        (uint64_t)d->channels * sv * 2 <= msda::kFwdStageLds;
-    if (staged) {
-      p.splits = (uint32_t)splits;
-      p.qper = (uint32_t)qper;
-      p.stage_bytes = msda::kFwdStageLds;
-      p.nblocks = (uint32_t)(slices * splits);
-    }
-    hipError_t e = (staged ? fn_staged : fn)(p, static_cast<hipStream_t>(stream));
-    if (e != hipSuccess) return fail(MSDA_ERR_HIP, "msda_fwd launch failed: %s", hipGetErrorString(e));
-  }
-  return MSDA_OK;
+int msda_fwd_fused(const msda_desc* d, const void* value, const int32_t* spatial_shapes,
+                   const int32_t* level_start, const float* reference_points,
+                   const void* sampling_offsets, const void* attention_logits, void* output,
+                   void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  return fwd_impl(d, value, spatial_shapes, level_start, sampling_offsets, attention_logits,
+                  reference_points, output, workspace, workspace_bytes, stream, true);
 }
 
 size_t msda_bwd_workspace_bytes(const msda_desc* d, const int32_t* host_spatial_shapes) {
@@ -564,6 +657,74 @@ int msda_bwd(const msda_desc* d, const int32_t* host_spatial_shapes, const void*
     if (e != hipSuccess) return fail(MSDA_ERR_HIP, "msda_bwd launch failed: %s", hipGetErrorString(e));
   }
   return MSDA_OK;
+}
+
+size_t msda_bwd_fused_workspace_bytes(const msda_desc* d, const int32_t* host_spatial_shapes) {
+  g_err[0] = 0;
+  if (validate(d)) return 0;
+  const uint64_t units = (uint64_t)d->batch * d->num_queries * d->num_heads;
+  if (units == 0 || d->num_levels == 0 || d->num_points == 0) return 0;
+  FusedWs w;
+  if (!fused_ws(d, host_spatial_shapes, &w)) return 0;
+  return (size_t)w.total;
+}
+
+int msda_bwd_fused(const msda_desc* d, const int32_t* host_spatial_shapes, const void* value,
+                   const float* reference_points, const void* sampling_offsets,
+                   const void* attention_logits, const void* grad_output, void* grad_value,
+                   float* grad_reference_points, void* grad_sampling_offsets,
+                   void* grad_attention_logits, void* workspace, size_t workspace_bytes,
+                   void* stream) {
+  g_err[0] = 0;
+  int rc = validate(d);
+  if (rc) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const uint64_t units = (uint64_t)d->batch * d->num_queries * d->num_heads;
+  const uint64_t nref = (uint64_t)d->batch * d->num_queries * d->num_levels * d->dim;
+  if (units == 0 || d->num_levels == 0 || d->num_points == 0) {
+    // no samples: grad_value and grad_reference_points are zero, the others empty
+    const size_t nval = (size_t)d->batch * (size_t)d->num_keys * d->num_heads * d->channels;
+    if ((nval && !grad_value) || (nref && !grad_reference_points))
+      return fail(MSDA_ERR_INVALID, "msda_bwd_fused: required pointer is NULL");
+    hipError_t e = msda::launch_zero_bytes(grad_value, nval * elem_bytes(d->value_dtype), st);
+    if (e == hipSuccess) e = msda::launch_zero_bytes(grad_reference_points, nref * 4, st);
+    if (e != hipSuccess) return fail(MSDA_ERR_HIP, "msda_bwd_fused clear failed: %s", hipGetErrorString(e));
+    return MSDA_OK;
+  }
+  if (!reference_points || !sampling_offsets || !attention_logits || !grad_reference_points ||
+      !grad_sampling_offsets || !grad_attention_logits)
+    return fail(MSDA_ERR_INVALID, "msda_bwd_fused: required pointer is NULL");
+  FusedWs w;
+  if (!fused_ws(d, host_spatial_shapes, &w)) return MSDA_ERR_INVALID;
+  if (!workspace || workspace_bytes < w.total)
+    return fail(MSDA_ERR_WORKSPACE, "msda_bwd_fused needs %llu workspace bytes, got %zu",
+                (unsigned long long)w.total, workspace_bytes);
+  if (((uintptr_t)workspace % 256) != 0)
+    return fail(MSDA_ERR_INVALID, "msda_bwd_fused: workspace must be 256-byte aligned");
+  char* ws = static_cast<char*>(workspace);
+  msda::FusedArgs a{};
+  a.ref = reference_points;
+  a.off = sampling_offsets;
+  a.logits = attention_logits;
+  a.loc = reinterpret_cast<float*>(ws + w.loc);
+  a.attn = reinterpret_cast<float*>(ws + w.attn);
+  // 1. the forward's fp32 locations and weights
+  if ((rc = run_fused_kernels(d, host_spatial_shapes, a, false, st))) return rc;
+  // 2. the ordinary backward on them
+  msda_desc d32 = *d;
+  d32.coord_dtype = MSDA_F32;
+  float* gloc = reinterpret_cast<float*>(ws + w.gloc);
+  float* gattn = reinterpret_cast<float*>(ws + w.gattn);
+  rc = msda_bwd(&d32, host_spatial_shapes, value, a.loc, a.attn, grad_output, grad_value, gloc,
+                gattn, ws + w.inner, w.total - w.inner, stream);
+  if (rc) return rc;
+  // 3. through the location and softmax formation
+  a.grad_loc = gloc;
+  a.grad_attn = gattn;
+  a.grad_ref = grad_reference_points;
+  a.grad_off = grad_sampling_offsets;
+  a.grad_logits = grad_attention_logits;
+  return run_fused_kernels(d, host_spatial_shapes, a, true, st);
 }
 
 }  // extern "C"

@@ -1,0 +1,126 @@
+// msda_fused.hip — producer-side kernels around the backward of the fused forward.
+//
+// The fused forward forms, per unit (b, q, h), in fp32:
+//   loc[b,q,h,l,p,d] = fma(off[b,q,h,l,p,d], inv_l[d], ref[b,q,l,d]),
+//                      inv_l = (1/W_l, 1/H_l[, 1/D_l]) rounded to fp32
+//   attn[b,q,h,l,p]  = exp(logit - max) * (1 / sum exp(logit - max)) over (l, p)
+// which is the location and weight formation of the reference modules
+// (src/msda_triton/pytorch/msda_2d.py:303-339, msda_3d.py:314-350) done inside the kernel.
+// Its backward runs the ordinary backward kernels on fp32 loc/attn written by
+// fused_prep_kernel, then fused_grad_kernel takes grad_loc / grad_attn through that
+// formation:
+//   grad_off    = grad_loc * inv_l
+//   grad_ref    = sum over (h, p) of grad_loc
+//   grad_logits = attn * (grad_attn - sum over (l, p) of attn * grad_attn)
+// Every output element is written once by one thread, in a fixed order of additions. The
+// locations are bit-identical to the forward's (same fma, same reciprocals); the weights
+// agree to rounding (the forward reduces the sum over its lanes, this kernel in order).
+#include "msda_internal.h"
+#include "msda_sample.h"
+
+namespace msda {
+
+namespace {
+
+template <typename E>
+__device__ inline float ld(const void* p, uint32_t i) {
+  return (float)static_cast<const typename E::T*>(p)[i];
+}
+
+template <typename E>
+__device__ inline void st(void* p, uint32_t i, float v) {
+  static_cast<typename E::T*>(p)[i] = (typename E::T)v;
+}
+
+// Indices are 32-bit: one launch covers a batch range whose units * L * P * 2^dim < 2^31.
+
+// Threads [0, units): one unit's weights (softmax, sequential over its L*P logits).
+// Threads [units, units + units*L*P): one sample's DIM coordinates each.
+template <int DIM, typename EI>
+__global__ __launch_bounds__(kBlock) void fused_prep_kernel(const FusedArgs a) {
+  const uint32_t LP = (uint32_t)(a.L * a.P);
+  const uint32_t t = blockIdx.x * kBlock + threadIdx.x;
+  if (t < a.units) {
+    const uint32_t o = t * LP;
+    float m = -INFINITY;
+    for (uint32_t s = 0; s < LP; ++s) m = fmaxf(m, ld<EI>(a.logits, o + s));
+    float sum = 0.0f;
+    for (uint32_t s = 0; s < LP; ++s) sum += expf(ld<EI>(a.logits, o + s) - m);
+    const float inv_sum = 1.0f / sum;
+    for (uint32_t s = 0; s < LP; ++s) a.attn[o + s] = expf(ld<EI>(a.logits, o + s) - m) * inv_sum;
+    return;
+  }
+  const uint32_t i = t - a.units;  // sample index (b, q, h, l, p)
+  if (i >= a.units * LP) return;
+  const uint32_t u = i / LP, lp = i - u * LP;
+  const uint32_t l = lp / (uint32_t)a.P, bq = u / (uint32_t)a.H;
+  const float* r = a.ref + (bq * (uint32_t)a.L + l) * DIM;
+#pragma unroll
+  for (int d = 0; d < DIM; ++d)
+    a.loc[i * DIM + d] = __builtin_fmaf(ld<EI>(a.off, i * DIM + d), a.inv[l][d], r[d]);
+}
+
+// Threads [0, units): one unit's logit gradients. Threads [units, units + units*L*P): one
+// sample's offset gradients. Threads beyond: one (b, q, l, d) reference-point gradient each,
+// summed over h then p.
+template <int DIM, typename EI>
+__global__ __launch_bounds__(kBlock) void fused_grad_kernel(const FusedArgs a) {
+  const uint32_t LP = (uint32_t)(a.L * a.P);
+  const uint32_t t = blockIdx.x * kBlock + threadIdx.x;
+  const uint32_t ns = a.units * LP;
+  if (t < a.units) {
+    const uint32_t o = t * LP;
+    float dot = 0.0f;
+    for (uint32_t s = 0; s < LP; ++s) dot += a.attn[o + s] * a.grad_attn[o + s];
+    for (uint32_t s = 0; s < LP; ++s)
+      st<EI>(a.grad_logits, o + s, a.attn[o + s] * (a.grad_attn[o + s] - dot));
+    return;
+  }
+  if (t < a.units + ns) {
+    const uint32_t i = t - a.units;
+    const uint32_t u = i / LP, lp = i - u * LP;
+    const uint32_t l = lp / (uint32_t)a.P;
+#pragma unroll
+    for (int d = 0; d < DIM; ++d)
+      st<EI>(a.grad_off, i * DIM + d, a.grad_loc[i * DIM + d] * a.inv[l][d]);
+    return;
+  }
+  const uint32_t j = t - a.units - ns;  // (b, q, l, d)
+  if (j >= a.bq * (uint32_t)a.L * DIM) return;
+  const uint32_t bql = j / DIM, d = j - bql * DIM;
+  const uint32_t bq = bql / (uint32_t)a.L, l = bql - bq * (uint32_t)a.L;
+  float g = 0.0f;
+  for (int h = 0; h < a.H; ++h) {
+    const uint32_t base = ((bq * (uint32_t)a.H + h) * LP + l * (uint32_t)a.P) * DIM + d;
+    for (int p = 0; p < a.P; ++p) g += a.grad_loc[base + (uint32_t)p * DIM];
+  }
+  a.grad_ref[j] = g;
+}
+
+template <int DIM, typename EI>
+hipError_t launch_both(const FusedArgs& a, bool grad, hipStream_t s) {
+  const uint64_t ns = (uint64_t)a.units * (uint64_t)(a.L * a.P);
+  const uint64_t n = a.units + ns + (grad ? (uint64_t)a.bq * a.L * DIM : 0);
+  if (n == 0) return hipSuccess;
+  const uint32_t blocks = (uint32_t)((n + kBlock - 1) / kBlock);
+  if (grad) hipLaunchKernelGGL((fused_grad_kernel<DIM, EI>), dim3(blocks), dim3(kBlock), 0, s, a);
+  else hipLaunchKernelGGL((fused_prep_kernel<DIM, EI>), dim3(blocks), dim3(kBlock), 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_fused(const FusedArgs& a, int dim, int cdt, bool grad, hipStream_t s) {
+  if (dim == 2) {
+    if (cdt == 0) return launch_both<2, F32>(a, grad, s);
+    if (cdt == 1) return launch_both<2, F16>(a, grad, s);
+    if (cdt == 2) return launch_both<2, BF16>(a, grad, s);
+  } else if (dim == 3) {
+    if (cdt == 0) return launch_both<3, F32>(a, grad, s);
+    if (cdt == 1) return launch_both<3, F16>(a, grad, s);
+    if (cdt == 2) return launch_both<3, BF16>(a, grad, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace msda

@@ -14,7 +14,7 @@
 //    share 128-byte lines of loc/attn/output run side by side; workgroups remapped so each
 //    XCD owns a contiguous unit range and keeps a (batch, head-group) value slice in its
 //    L2. Corners outside the level read as zero through the buffer range check.
-//  * msda_fwd_staged_kernel: one 1024-thread workgroup per CU serves one (batch, head) and
+//  * msda_fwd_staged_kernel: one 768-thread workgroup per CU serves one (batch, head) and
 //    a range of queries. It first copies the smallest levels of that (batch, head) value
 //    slice that fit kFwdStageLds into LDS; corners on those levels are then read from LDS,
 //    the others from L2 (their slices again XCD-resident). Every row gather goes to L2 as a
@@ -56,6 +56,7 @@ struct FwdLevel {
   uint32_t base;           // global: start * rs; staged: first LDS byte of the level
   int32_t sx, sy, sz;      // byte strides along x, y, z
   int32_t flags;           // kLvlStaged | kLvlMul24
+  float inv[3];            // 1 / W, 1 / H, 1 / D (fused producer path)
 };
 constexpr int32_t kLvlStaged = 1;  // rows are in LDS
 constexpr int32_t kLvlMul24 = 2;   // strides and extents fit 24-bit signed multiplies
@@ -101,6 +102,9 @@ __device__ inline void stage_levels(const Params& p, FwdLevel* s_lvl, uint32_t r
     }
     e.base = (uint32_t)e.start * rs;
     e.flags = 0;
+    e.inv[0] = 1.0f / (float)e.W;
+    e.inv[1] = 1.0f / (float)e.H;
+    e.inv[2] = 1.0f / (float)e.D;
     set_strides<DIM>(e, rs);
     s_lvl[i] = e;
   }
@@ -174,10 +178,76 @@ __device__ inline uint32_t quad_bcast(uint32_t x) {
   return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, K * 0x55, 0xF, 0xF, true);
 }
 
-template <int DIM, typename EV, typename EC, int VEC, int PT, bool STAGED, bool SHARE = false>
+// Value x of lane j of the unit's lane group (first lane gbase), for j < nvec.
+__device__ inline float group_lane(int gbase, int j, float x) {
+  return as_float((uint32_t)__builtin_amdgcn_ds_bpermute((gbase + j) << 2, (int)as_u32(x)));
+}
+
+// Fused producer path: the unit's offset and logit blocks are held like location and weight
+// blocks (coord dtype EC); each sample's location and weight are formed when its batch is
+// used:
+//   loc[d] = fma(off[d], 1 / size_l[d], ref[l][d]),   size_l = (W, H[, D]) of its level l
+//   attn   = exp(logit - max) * (1 / sum exp(logit - max))   over the unit's L*P logits
+// FusedStats holds the unit's max and 1/sum, reduced over its lanes in lane order (so every
+// lane of the unit uses the same two values), and lane j's copy of the reference point of
+// level j (used when L <= nvec; otherwise the reference points are read per batch).
+template <int DIM>
+struct FusedStats {
+  float m, inv_sum;
+  float ref[DIM];
+};
+
+template <int DIM, typename EC, int SB, int NS>
+__device__ inline FusedStats<DIM> fused_stats(const Params& p, uint32_t bq, uint32_t lane,
+                                              int nbatch, int gbase,
+                                              const CoordBlock<EC, SB> (&ha)[NS]) {
+  const int nv = p.nvec;
+  FusedStats<DIM> st;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int sl = 0; sl < NS; ++sl)
+    if ((int)lane + sl * nv < nbatch)
+#pragma unroll
+      for (int k = 0; k < SB; ++k) mx = fmaxf(mx, block_elem(ha[sl], k));
+  st.m = -INFINITY;
+  for (int j = 0; j < nv; ++j) st.m = fmaxf(st.m, group_lane(gbase, j, mx));
+  float ls = 0.0f;
+#pragma unroll
+  for (int sl = 0; sl < NS; ++sl)
+    if ((int)lane + sl * nv < nbatch)
+#pragma unroll
+      for (int k = 0; k < SB; ++k) ls += expf(block_elem(ha[sl], k) - st.m);
+  float sum = 0.0f;
+  for (int j = 0; j < nv; ++j) sum += group_lane(gbase, j, ls);
+  st.inv_sum = 1.0f / sum;
+  const float* refp = p.ref + (size_t)bq * (uint32_t)(p.L * DIM);
+#pragma unroll
+  for (int d = 0; d < DIM; ++d) st.ref[d] = (int)lane < p.L ? refp[lane * DIM + d] : 0.0f;
+  return st;
+}
+
+// Reference point of level l for the unit (uniform l): from lane l of the group, or from
+// memory when the levels outnumber the lanes.
+template <int DIM>
+__device__ inline void fused_ref(const Params& p, const FusedStats<DIM>& st, uint32_t bq, int gbase,
+                                 int l, float (&r)[DIM]) {
+  if (p.L <= p.nvec) {
+#pragma unroll
+    for (int d = 0; d < DIM; ++d) r[d] = group_lane(gbase, l, st.ref[d]);
+  } else {
+    const float* refp = p.ref + (size_t)bq * (uint32_t)(p.L * DIM) + l * DIM;
+#pragma unroll
+    for (int d = 0; d < DIM; ++d) r[d] = refp[d];
+  }
+}
+
+// FUSED: p.loc / p.attn hold offsets and logits and p.ref the reference points (see
+// Params); bq = b * Q + q indexes the unit's reference points.
+template <int DIM, typename EV, typename EC, int VEC, int PT, bool STAGED, bool SHARE = false,
+          bool FUSED = false>
 __device__ inline void unit_forward(const Params& p, const FwdLevel* s_lvl, const char* s_rows,
                                     uint32_t zoff, uint32_t b, uint32_t h, uint32_t bqh,
-                                    uint32_t lane, float (&acc)[VEC]) {
+                                    uint32_t bq, uint32_t lane, float (&acc)[VEC]) {
   constexpr int VB = VEC * EV::kBytes;
   constexpr int NC = 1 << DIM;
   constexpr int SB = PT > 0 ? (DIM == 2 ? (PT < 4 ? PT : 4) : (PT < 2 ? PT : 2)) : (DIM == 2 ? 4 : 2);
@@ -203,6 +273,7 @@ __device__ inline void unit_forward(const Params& p, const FwdLevel* s_lvl, cons
     const int nv = p.nvec;
     CoordBlock<EC, SB * DIM> hl[kFwdCoordSlots<DIM>];
     CoordBlock<EC, SB> ha[kFwdCoordSlots<DIM>];
+    const int gbase = (int)(__lane_id() & ~((1u << p.lpu_log2) - 1u));  // first lane of the group
 #pragma unroll
     for (int sl = 0; sl < kFwdCoordSlots<DIM>; ++sl) {
       const int bj = (int)lane + sl * nv;
@@ -211,7 +282,8 @@ __device__ inline void unit_forward(const Params& p, const FwdLevel* s_lvl, cons
         load_block<EC, SB>(ha[sl], attp + bj * SB);
       }
     }
-    const int gbase = (int)(__lane_id() & ~((1u << p.lpu_log2) - 1u));  // first lane of the group
+    FusedStats<DIM> fst;
+    if constexpr (FUSED) fst = fused_stats<DIM, EC, SB, kFwdCoordSlots<DIM>>(p, bq, lane, nbatch, gbase, ha);
     if constexpr (SHARE) {
       const int ks = (int)(lane & 3u) % SB;  // the batch sample this lane computes
       const uint32_t vbase0 = vbase - lane_off;
@@ -247,6 +319,13 @@ __device__ inline void unit_forward(const Params& p, const FwdLevel* s_lvl, cons
           a = ks == k ? block_elem(ab, k) : a;
 #pragma unroll
           for (int d = 0; d < DIM; ++d) xyz[d] = ks == k ? block_elem(lb, k * DIM + d) : xyz[d];
+        }
+        if constexpr (FUSED) {
+          float r[DIM];
+          fused_ref<DIM>(p, fst, bq, gbase, l, r);
+#pragma unroll
+          for (int d = 0; d < DIM; ++d) xyz[d] = __builtin_fmaf(xyz[d], lv.inv[d], r[d]);
+          a = expf(a - fst.m) * fst.inv_sum;
         }
         Sample<DIM> sm;
         sm.ax = make_axis(xyz[0], (float)lv.W, lv.W, p.clamp, p.lo_g, p.hi_g);
@@ -340,13 +419,21 @@ __device__ inline void unit_forward(const Params& p, const FwdLevel* s_lvl, cons
       }
       Sample<DIM> sm[SB];
       float cw[SB][NC];
+      float r[DIM];
+      if constexpr (FUSED) fused_ref<DIM>(p, fst, bq, gbase, l, r);
 #pragma unroll
       for (int k = 0; k < SB; ++k) {
-        sm[k].ax = make_axis(block_elem(lb, k * DIM + 0), (float)lv.W, lv.W, p.clamp, p.lo_g, p.hi_g);
-        sm[k].ay = make_axis(block_elem(lb, k * DIM + 1), (float)lv.H, lv.H, p.clamp, p.lo_g, p.hi_g);
-        if constexpr (DIM == 3)
-          sm[k].az = make_axis(block_elem(lb, k * DIM + 2), (float)lv.D, lv.D, p.clamp, p.lo_g, p.hi_g);
-        const float a = block_elem(ab, k);
+        float xyz[DIM], a = block_elem(ab, k);
+#pragma unroll
+        for (int d = 0; d < DIM; ++d) xyz[d] = block_elem(lb, k * DIM + d);
+        if constexpr (FUSED) {
+#pragma unroll
+          for (int d = 0; d < DIM; ++d) xyz[d] = __builtin_fmaf(xyz[d], lv.inv[d], r[d]);
+          a = expf(a - fst.m) * fst.inv_sum;
+        }
+        sm[k].ax = make_axis(xyz[0], (float)lv.W, lv.W, p.clamp, p.lo_g, p.hi_g);
+        sm[k].ay = make_axis(xyz[1], (float)lv.H, lv.H, p.clamp, p.lo_g, p.hi_g);
+        if constexpr (DIM == 3) sm[k].az = make_axis(xyz[2], (float)lv.D, lv.D, p.clamp, p.lo_g, p.hi_g);
 #pragma unroll
         for (int c = 0; c < NC; ++c) cw[k][c] = corner_weight<DIM>(c, sm[k]) * a;
       }
@@ -364,6 +451,16 @@ __device__ inline void unit_forward(const Params& p, const FwdLevel* s_lvl, cons
       }
     }
   } else {
+    // FUSED: softmax statistics of the unit's logits, each lane over all of them
+    float smax = 0.0f, inv_sum = 1.0f;
+    if constexpr (FUSED) {
+      smax = -INFINITY;
+      for (int s = 0; s < LP; ++s) smax = fmaxf(smax, (float)attp[s]);
+      float ssum = 0.0f;
+      for (int s = 0; s < LP; ++s) ssum += expf((float)attp[s] - smax);
+      inv_sum = 1.0f / ssum;
+    }
+    const float* refp = FUSED ? p.ref + (size_t)bq * (uint32_t)(p.L * DIM) : nullptr;
     for (int l = 0; l < p.L; ++l) {
       const FwdLevel lv = s_lvl[l];
       for (int p0 = 0; p0 < p.P; p0 += SB) {
@@ -373,11 +470,20 @@ __device__ inline void unit_forward(const Params& p, const FwdLevel* s_lvl, cons
         for (int k = 0; k < SB; ++k) {
           const int s = l * p.P + p0 + k;
           const bool live = p0 + k < p.P;
-          const float a = live ? (float)attp[s] : 0.0f;
           const TC* lp = locp + (live ? s : 0) * DIM;
-          sm[k].ax = make_axis((float)lp[0], (float)lv.W, lv.W, p.clamp, p.lo_g, p.hi_g);
-          sm[k].ay = make_axis((float)lp[1], (float)lv.H, lv.H, p.clamp, p.lo_g, p.hi_g);
-          if constexpr (DIM == 3) sm[k].az = make_axis((float)lp[2], (float)lv.D, lv.D, p.clamp, p.lo_g, p.hi_g);
+          float a, xyz[DIM];
+          if constexpr (FUSED) {
+            a = live ? expf((float)attp[s] - smax) * inv_sum : 0.0f;
+#pragma unroll
+            for (int d = 0; d < DIM; ++d) xyz[d] = __builtin_fmaf((float)lp[d], lv.inv[d], refp[l * DIM + d]);
+          } else {
+            a = live ? (float)attp[s] : 0.0f;
+#pragma unroll
+            for (int d = 0; d < DIM; ++d) xyz[d] = (float)lp[d];
+          }
+          sm[k].ax = make_axis(xyz[0], (float)lv.W, lv.W, p.clamp, p.lo_g, p.hi_g);
+          sm[k].ay = make_axis(xyz[1], (float)lv.H, lv.H, p.clamp, p.lo_g, p.hi_g);
+          if constexpr (DIM == 3) sm[k].az = make_axis(xyz[2], (float)lv.D, lv.D, p.clamp, p.lo_g, p.hi_g);
 #pragma unroll
           for (int c = 0; c < NC; ++c) cw[k][c] = corner_weight<DIM>(c, sm[k]) * a;
         }
@@ -406,7 +512,7 @@ __device__ inline void unit_forward(const Params& p, const FwdLevel* s_lvl, cons
 // Replaces the reference's _fwd_kernel_2d (src/msda_triton/triton/msda_2d.py:85-260) and
 // _fwd_kernel (src/msda_triton/triton/msda_3d.py:80-288). Writes (B, Q, H*C) in the value
 // dtype directly instead of an fp32 (B*H, Q, C) scratch plus permute (msda_2d.py:649-651).
-template <int DIM, typename EV, typename EC, int VEC, int PT>
+template <int DIM, typename EV, typename EC, int VEC, int PT, bool FUSED>
 __global__ __launch_bounds__(kBlock) void msda_fwd_kernel(const Params p) {
   __shared__ FwdLevel s_lvl[kMaxLevels];
   stage_levels<DIM>(p, s_lvl, row_stride(p, EV::kBytes));
@@ -415,14 +521,15 @@ __global__ __launch_bounds__(kBlock) void msda_fwd_kernel(const Params p) {
   if (!decode_unit(p, u)) return;
   if ((int)u.lane >= p.nvec) return;
   float acc[VEC];
-  unit_forward<DIM, EV, EC, VEC, PT, false>(p, s_lvl, nullptr, 0u, u.b, u.h, u.bqh, u.lane, acc);
+  unit_forward<DIM, EV, EC, VEC, PT, false, false, FUSED>(p, s_lvl, nullptr, 0u, u.b, u.h, u.bqh,
+                                                         u.b * p.Q + u.q, u.lane, acc);
   typename EV::T* outp = static_cast<typename EV::T*>(p.out) + (size_t)u.bqh * p.C + u.lane * VEC;
   store_vec<EV, VEC>(outp, acc);
 }
 
 // Same result as msda_fwd_kernel; the smallest levels of the workgroup's (batch, head)
 // value slice are read from LDS.
-template <int DIM, typename EV, typename EC, int VEC, int PT, bool SHARE>
+template <int DIM, typename EV, typename EC, int VEC, int PT, bool SHARE, bool FUSED>
 __global__ __launch_bounds__(kFwdStageThreads) void msda_fwd_staged_kernel(const Params p) {
   constexpr int NT = kFwdStageThreads;
   constexpr int VB = VEC * EV::kBytes;
@@ -519,7 +626,8 @@ __global__ __launch_bounds__(kFwdStageThreads) void msda_fwd_staged_kernel(const
     if (q >= q1) break;
     const uint32_t bqh = (b * p.Q + q) * (uint32_t)p.H + h;
     float acc[VEC];
-    unit_forward<DIM, EV, EC, VEC, PT, true, SHARE>(p, s_lvl, s_rows, zrow + lane * VB, b, h, bqh, lane, acc);
+    unit_forward<DIM, EV, EC, VEC, PT, true, SHARE, FUSED>(p, s_lvl, s_rows, zrow + lane * VB, b, h, bqh,
+                                                           b * p.Q + q, lane, acc);
     typename EV::T* outp = static_cast<typename EV::T*>(p.out) + (size_t)bqh * p.C + lane * VEC;
     store_vec<EV, VEC>(outp, acc);
   }
@@ -533,56 +641,56 @@ static bool pt_path(const Params& p) {
   return p.P == PT && p.coords_aligned && p.L * (PT / SB) <= kFwdCoordSlots<DIM> * p.nvec;
 }
 
-template <int DIM, typename EV, typename EC, int VEC>
+template <int DIM, typename EV, typename EC, int VEC, bool FUSED>
 static hipError_t launch_fwd(const Params& p, hipStream_t s) {
   if (pt_path<DIM, 4>(p))
-    hipLaunchKernelGGL((msda_fwd_kernel<DIM, EV, EC, VEC, 4>), dim3(p.nblocks), dim3(kBlock), 0, s, p);
+    hipLaunchKernelGGL((msda_fwd_kernel<DIM, EV, EC, VEC, 4, FUSED>), dim3(p.nblocks), dim3(kBlock), 0, s, p);
   else if (pt_path<DIM, 8>(p))
-    hipLaunchKernelGGL((msda_fwd_kernel<DIM, EV, EC, VEC, 8>), dim3(p.nblocks), dim3(kBlock), 0, s, p);
+    hipLaunchKernelGGL((msda_fwd_kernel<DIM, EV, EC, VEC, 8, FUSED>), dim3(p.nblocks), dim3(kBlock), 0, s, p);
   else
-    hipLaunchKernelGGL((msda_fwd_kernel<DIM, EV, EC, VEC, 0>), dim3(p.nblocks), dim3(kBlock), 0, s, p);
+    hipLaunchKernelGGL((msda_fwd_kernel<DIM, EV, EC, VEC, 0, FUSED>), dim3(p.nblocks), dim3(kBlock), 0, s, p);
   return hipGetLastError();
 }
 
-template <int DIM, typename EV, typename EC, int VEC>
+template <int DIM, typename EV, typename EC, int VEC, bool FUSED>
 static hipError_t launch_fwd_staged(const Params& p, hipStream_t s) {
   const dim3 g(p.nblocks), t(kFwdStageThreads);
   // quad-shared geometry when every lane of a unit's 4-lane quads is active
   const bool share = p.lpu_log2 >= 2 && p.nvec == (1 << p.lpu_log2);
   if (pt_path<DIM, 4>(p) && share)
-    hipLaunchKernelGGL((msda_fwd_staged_kernel<DIM, EV, EC, VEC, 4, true>), g, t, p.stage_bytes, s, p);
+    hipLaunchKernelGGL((msda_fwd_staged_kernel<DIM, EV, EC, VEC, 4, true, FUSED>), g, t, p.stage_bytes, s, p);
   else if (pt_path<DIM, 8>(p) && share)
-    hipLaunchKernelGGL((msda_fwd_staged_kernel<DIM, EV, EC, VEC, 8, true>), g, t, p.stage_bytes, s, p);
+    hipLaunchKernelGGL((msda_fwd_staged_kernel<DIM, EV, EC, VEC, 8, true, FUSED>), g, t, p.stage_bytes, s, p);
   else if (pt_path<DIM, 4>(p))
-    hipLaunchKernelGGL((msda_fwd_staged_kernel<DIM, EV, EC, VEC, 4, false>), g, t, p.stage_bytes, s, p);
+    hipLaunchKernelGGL((msda_fwd_staged_kernel<DIM, EV, EC, VEC, 4, false, FUSED>), g, t, p.stage_bytes, s, p);
   else if (pt_path<DIM, 8>(p))
-    hipLaunchKernelGGL((msda_fwd_staged_kernel<DIM, EV, EC, VEC, 8, false>), g, t, p.stage_bytes, s, p);
+    hipLaunchKernelGGL((msda_fwd_staged_kernel<DIM, EV, EC, VEC, 8, false, FUSED>), g, t, p.stage_bytes, s, p);
   else
-    hipLaunchKernelGGL((msda_fwd_staged_kernel<DIM, EV, EC, VEC, 0, false>), g, t, p.stage_bytes, s, p);
+    hipLaunchKernelGGL((msda_fwd_staged_kernel<DIM, EV, EC, VEC, 0, false, FUSED>), g, t, p.stage_bytes, s, p);
   return hipGetLastError();
 }
 
-template <int DIM, typename EV, typename EC>
+template <int DIM, typename EV, typename EC, bool FUSED>
 static LaunchFn pick_vec(int vec_bytes, bool staged) {
   constexpr int S = EV::kBytes;
   switch (vec_bytes) {
-    case 16: return staged ? &launch_fwd_staged<DIM, EV, EC, 16 / S> : &launch_fwd<DIM, EV, EC, 16 / S>;
-    case 8: return staged ? &launch_fwd_staged<DIM, EV, EC, 8 / S> : &launch_fwd<DIM, EV, EC, 8 / S>;
-    case 4: return staged ? &launch_fwd_staged<DIM, EV, EC, 4 / S> : &launch_fwd<DIM, EV, EC, 4 / S>;
+    case 16: return staged ? &launch_fwd_staged<DIM, EV, EC, 16 / S, FUSED> : &launch_fwd<DIM, EV, EC, 16 / S, FUSED>;
+    case 8: return staged ? &launch_fwd_staged<DIM, EV, EC, 8 / S, FUSED> : &launch_fwd<DIM, EV, EC, 8 / S, FUSED>;
+    case 4: return staged ? &launch_fwd_staged<DIM, EV, EC, 4 / S, FUSED> : &launch_fwd<DIM, EV, EC, 4 / S, FUSED>;
     case 2:
-      if constexpr (S == 2) return staged ? &launch_fwd_staged<DIM, EV, EC, 1> : &launch_fwd<DIM, EV, EC, 1>;
+      if constexpr (S == 2) return staged ? &launch_fwd_staged<DIM, EV, EC, 1, FUSED> : &launch_fwd<DIM, EV, EC, 1, FUSED>;
       return nullptr;
     default: return nullptr;
   }
 }
 
-template <int DIM>
+template <int DIM, bool FUSED>
 static LaunchFn pick_types(int vdt, int cdt, int vec_bytes, bool staged) {
-  if (vdt == 0 && cdt == 0) return pick_vec<DIM, F32, F32>(vec_bytes, staged);
-  if (vdt == 1 && cdt == 1) return pick_vec<DIM, F16, F16>(vec_bytes, staged);
-  if (vdt == 1 && cdt == 0) return pick_vec<DIM, F16, F32>(vec_bytes, staged);
-  if (vdt == 2 && cdt == 2) return pick_vec<DIM, BF16, BF16>(vec_bytes, staged);
-  if (vdt == 2 && cdt == 0) return pick_vec<DIM, BF16, F32>(vec_bytes, staged);
+  if (vdt == 0 && cdt == 0) return pick_vec<DIM, F32, F32, FUSED>(vec_bytes, staged);
+  if (vdt == 1 && cdt == 1) return pick_vec<DIM, F16, F16, FUSED>(vec_bytes, staged);
+  if (vdt == 1 && cdt == 0) return pick_vec<DIM, F16, F32, FUSED>(vec_bytes, staged);
+  if (vdt == 2 && cdt == 2) return pick_vec<DIM, BF16, BF16, FUSED>(vec_bytes, staged);
+  if (vdt == 2 && cdt == 0) return pick_vec<DIM, BF16, F32, FUSED>(vec_bytes, staged);
   return nullptr;
 }
 
@@ -623,9 +731,9 @@ hipError_t launch_head_major(const void* src, void* dst, uint32_t B, uint32_t K,
   return hipGetLastError();
 }
 
-LaunchFn get_fwd_launcher(int dim, int vdt, int cdt, int vec_bytes, bool staged) {
-  if (dim == 2) return pick_types<2>(vdt, cdt, vec_bytes, staged);
-  if (dim == 3) return pick_types<3>(vdt, cdt, vec_bytes, staged);
+LaunchFn get_fwd_launcher(int dim, int vdt, int cdt, int vec_bytes, bool staged, bool fused) {
+  if (dim == 2) return fused ? pick_types<2, true>(vdt, cdt, vec_bytes, staged) : pick_types<2, false>(vdt, cdt, vec_bytes, staged);
+  if (dim == 3) return fused ? pick_types<3, true>(vdt, cdt, vec_bytes, staged) : pick_types<3, false>(vdt, cdt, vec_bytes, staged);
   return nullptr;
 }
 

@@ -19,7 +19,10 @@ constexpr int kTileWavesPerSimd = 4;  // tile-kernel occupancy target: two workg
 constexpr int kFillStage = 2048;      // records staged in LDS per fill round
 constexpr int kGradThreads = 256;     // threads of the backward sample-gradient kernel
 constexpr int kGradRounds = 4;        // unit groups each of its threads handles in turn
-constexpr int kFwdStageThreads = 1024;            // threads of the staged forward kernel
+// threads of the staged forward kernel: 12 waves per CU leave each lane 168 VGPRs, so
+// neither variant spills (at 1024 threads, 128 VGPRs, the plain kernel spilled 20-64 bytes
+// per lane and the fused one 70-116, and both ran slower; 512 and 896 threads were slower)
+constexpr int kFwdStageThreads = 768;
 constexpr uint32_t kFwdStageLds = 156 * 1024;     // its dynamic LDS: one workgroup per CU
 constexpr uint32_t kFwdStageMinQueries = 512;     // queries per workgroup that pay for staging
 // coordinate blocks a forward lane holds (2D: 4-sample blocks, 3D: 2-sample blocks)
@@ -56,6 +59,11 @@ struct Params {
   // head-major copy of value, (Bc, H, K, C), or nullptr: rows are then read from it with
   // the rows of one head contiguous
   const void* value_h;
+  // fused producer launches: loc holds the sampling offsets (Bc, Q, H, L, P, dim) and attn
+  // the attention logits (Bc, Q, H, L, P), both coord_dtype; ref the fp32 reference points
+  // (Bc, Q, L, dim). The kernel forms loc = ref + off / (W, H[, D]) and attn = softmax over
+  // (L, P) in fp32.
+  const float* ref;
 };
 
 using LaunchFn = hipError_t (*)(const Params&, hipStream_t);
@@ -66,8 +74,9 @@ hipError_t launch_head_major(const void* src, void* dst, uint32_t B, uint32_t K,
                              uint32_t row_bytes, int vec_bytes, hipStream_t s);
 
 // Forward launcher for (dim, value dtype, coord dtype, bytes per lane load), or nullptr.
-// `staged` selects the kernel that serves small levels from LDS (Params.splits/qper set).
-LaunchFn get_fwd_launcher(int dim, int vdt, int cdt, int vec_bytes, bool staged);
+// `staged` selects the kernel that serves small levels from LDS (Params.splits/qper set);
+// `fused` the kernels that form locations and weights from offsets and logits (Params.ref).
+LaunchFn get_fwd_launcher(int dim, int vdt, int cdt, int vec_bytes, bool staged, bool fused);
 
 // ---------------------------------------------------------------------------------------
 // Backward. grad_value is accumulated in key order. Every sample with a valid corner is
@@ -168,5 +177,29 @@ hipError_t run_bwd(const BwdPlan& pl, const BwdBuffers& bf, int dim, int vdt, in
                    int vec_bytes, hipStream_t s);
 
 bool bwd_supported(int dim, int vdt, int cdt, int vec_bytes);
+
+// ---------------------------------------------------------------------------------------
+// Producer-side kernels of the fused path's backward (msda_fused.hip), for one launch over
+// a batch range (units * L * P * 2^dim < 2^31).
+struct FusedArgs {
+  const float* ref;         // (Bc, Q, L, dim) fp32
+  const void* off;          // (Bc, Q, H, L, P, dim) coord dtype
+  const void* logits;       // (Bc, Q, H, L, P) coord dtype
+  float* loc;               // (Bc, Q, H, L, P, dim) fp32, written by the prep kernel
+  float* attn;              // (Bc, Q, H, L, P) fp32, written by the prep kernel
+  const float* grad_loc;    // fp32 gradients from the backward kernels
+  const float* grad_attn;
+  float* grad_ref;          // (Bc, Q, L, dim) fp32
+  void* grad_off;           // coord dtype
+  void* grad_logits;        // coord dtype
+  uint32_t units;           // Bc * Q * H
+  uint32_t bq;              // Bc * Q
+  int32_t H, L, P;
+  float inv[kMaxLevels][3];   // 1/W, 1/H, 1/D per level (fp32, correctly rounded)
+};
+
+// grad == false: loc and attn from ref, off and logits. grad == true: grad_ref, grad_off and
+// grad_logits from grad_loc, grad_attn and attn. cdt is the coord dtype code.
+hipError_t launch_fused(const FusedArgs& a, int dim, int cdt, bool grad, hipStream_t s);
 
 }  // namespace msda

@@ -3,9 +3,11 @@
 Same constructor, parameters, ``init_weights`` patterns and ``forward`` contract as the
 reference modules (src/msda_triton/pytorch/msda_2d.py:117-383, msda_3d.py:121-394), which
 run the pure-PyTorch function; these run ``msda2d`` / ``msda3d`` (libmsda_hip.so) for the
-sampling step, so their tensors must be on the GPU. The surrounding projections, softmax,
-location formation, masking, chunking, checkpointing, dropout and residual are plain
-PyTorch, as in the reference.
+sampling step, so their tensors must be on the GPU. The projections, masking, chunking, checkpointing, dropout and residual are plain PyTorch,
+as in the reference. With ``fused=True`` (the default) the softmax over L*P and the location
+formation ``reference + offset / (W, H[, D])`` run inside the HIP kernel (``msda2d_fused`` /
+``msda3d_fused``) instead of as separate PyTorch ops; ``fused=False`` keeps the reference's
+order of operations.
 """
 
 from __future__ import annotations
@@ -16,6 +18,7 @@ import torch
 from torch import nn
 from torch.utils.checkpoint import checkpoint
 
+from msda_triton.hip.fused import msda2d_fused, msda3d_fused
 from msda_triton.hip.msda_2d import msda2d
 from msda_triton.hip.msda_3d import msda3d
 
@@ -29,7 +32,7 @@ class _MSDAModule(nn.Module):
                  dropout: float = 0.1, batch_first: bool = False,
                  query_chunk_size: int | None = None, head_chunk_size: int | None = None,
                  use_checkpoint: bool = False, clamp_grid: bool = True,
-                 clamp_eps: float = 1e-4, **kwargs) -> None:
+                 clamp_eps: float = 1e-4, fused: bool = True, **kwargs) -> None:
         super().__init__()
         if embed_dims % num_heads != 0:
             raise ValueError(
@@ -45,16 +48,22 @@ class _MSDAModule(nn.Module):
         self.use_checkpoint = use_checkpoint
         self.clamp_grid = clamp_grid
         self.clamp_eps = clamp_eps
+        self.fused = fused
         d = self.dim
         self.sampling_offsets = nn.Linear(embed_dims, num_heads * num_levels * num_points * d)
         self.attention_weights = nn.Linear(embed_dims, num_heads * num_levels * num_points)
         self.value_proj = nn.Linear(embed_dims, embed_dims)
         self.output_proj = nn.Linear(embed_dims, embed_dims)
 
-    # the sampling op (msda2d / msda3d); a test may substitute another function
+    # the sampling ops (msda2d / msda3d and their fused variants); a test may substitute
+    # other functions
     def _msda(self, value, shapes, loc, attn):
         op = msda2d if self.dim == 2 else msda3d
         return op(value, shapes, loc, attn, self.clamp_grid, self.clamp_eps)
+
+    def _msda_fused(self, value, shapes, ref, off, logits):
+        op = msda2d_fused if self.dim == 2 else msda3d_fused
+        return op(value, shapes, ref, off, logits, self.clamp_grid, self.clamp_eps)
 
     def _offset_bias(self, device) -> torch.Tensor:  # (H, L, P, dim)
         raise NotImplementedError
@@ -108,7 +117,7 @@ class _MSDAModule(nn.Module):
         # per-level extents in coordinate order (x, y[, z]) = (W, H[, D]); kept integer so
         # the offsets keep their dtype in the division, as in the reference. The shapes may
         # stay on the host (the op's fastest form); the normalizer goes to the offsets.
-        normalizer = spatial_shapes.flip(-1).to(reference_points.device)
+        normalizer = None if self.fused else spatial_shapes.flip(-1).to(reference_points.device)
 
         H, L, P = self.num_heads, self.num_levels, self.num_points
         qc = int(self.query_chunk_size) if self.query_chunk_size else nq
@@ -120,17 +129,25 @@ class _MSDAModule(nn.Module):
             q1 = min(q0 + qc, nq)
             qq = q[:, q0:q1]
             off = self.sampling_offsets(qq).view(bs, q1 - q0, H, L, P, d)
-            attn = self.attention_weights(qq).view(bs, q1 - q0, H, L * P).softmax(-1)
-            attn = attn.view(bs, q1 - q0, H, L, P)
-            loc = reference_points[:, q0:q1, None, :, None, :] + off / normalizer[None, None, None, :, None, :]
+            logits = self.attention_weights(qq).view(bs, q1 - q0, H, L, P)
+            if self.fused:
+                ref = reference_points[:, q0:q1]
+                fn = self._msda_fused
+            else:
+                attn = logits.view(bs, q1 - q0, H, L * P).softmax(-1).view(bs, q1 - q0, H, L, P)
+                loc = reference_points[:, q0:q1, None, :, None, :] + off / normalizer[None, None, None, :, None, :]
+                fn = self._msda
             out = q.new_zeros(bs, q1 - q0, self.embed_dims)
             for h0 in range(0, H, hc):
                 h1 = min(h0 + hc, H)
-                args = (v[:, :, h0:h1], spatial_shapes, loc[:, :, h0:h1], attn[:, :, h0:h1])
-                if self.use_checkpoint and self.training:
-                    o = checkpoint(self._msda, *args, use_reentrant=False)
+                if self.fused:
+                    args = (v[:, :, h0:h1], spatial_shapes, ref, off[:, :, h0:h1], logits[:, :, h0:h1])
                 else:
-                    o = self._msda(*args)
+                    args = (v[:, :, h0:h1], spatial_shapes, loc[:, :, h0:h1], attn[:, :, h0:h1])
+                if self.use_checkpoint and self.training:
+                    o = checkpoint(fn, *args, use_reentrant=False)
+                else:
+                    o = fn(*args)
                 out[:, :, h0 * dph:h1 * dph] = o
             outs.append(out)
         output = self.output_proj(torch.cat(outs, dim=1))

@@ -12,6 +12,12 @@ dtype, so its rounding matches the reference oracle's:
 4. multiply by the level's attention weights, sum over points, accumulate over levels in
    an accumulator of the input dtype (msda_2d.py:71, 102-110);
 5. return (B, Q, H*C) (msda_2d.py:113-114).
+
+``msda_fused_ref`` restates the attention modules' formation of locations and weights
+before that call (pytorch/msda_2d.py:303-339, pytorch/msda_3d.py:314-350): the offset
+normaliser stacks the level extents in coordinate order (W, H[, D]); locations are
+reference_points[:, :, None, :, None, :] + offsets / normaliser; weights are the softmax of
+the logits over the flattened L*P axis.
 """
 
 from __future__ import annotations
@@ -55,3 +61,19 @@ def msda_ref_grads(value, shapes, loc, attn, grad_out, clamp_grid=True, clamp_ep
     out = msda_ref(v, shapes, lo, a, clamp_grid, clamp_eps)
     out.backward(grad_out.to(out.dtype))
     return out.detach(), v.grad, lo.grad, a.grad
+
+
+def msda_fused_ref(value: torch.Tensor, value_spatial_shapes: torch.Tensor,
+                   reference_points: torch.Tensor, sampling_offsets: torch.Tensor,
+                   attention_logits: torch.Tensor, clamp_grid: bool = True,
+                   clamp_eps: float = 1e-4) -> torch.Tensor:
+    """msda_ref of the locations and weights formed from (B, Q, L, d) reference points,
+    (B, Q, H, L, P, d) offsets and (B, Q, H, L, P) logits, as the modules form them."""
+    bs, nq, nh, nl, npt, dim = sampling_offsets.shape
+    shapes = value_spatial_shapes.to(torch.int64)
+    # (L, d) in coordinate order: 2D (W, H) = columns (1, 0); 3D (W, H, D) = (2, 1, 0)
+    normalizer = torch.stack([shapes[..., dim - 1 - k] for k in range(dim)], -1)
+    attn = attention_logits.reshape(bs, nq, nh, nl * npt).softmax(-1).view(bs, nq, nh, nl, npt)
+    loc = (reference_points[:, :, None, :, None, :]
+           + sampling_offsets / normalizer[None, None, None, :, None, :])
+    return msda_ref(value, value_spatial_shapes, loc, attn, clamp_grid, clamp_eps)

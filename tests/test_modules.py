@@ -7,7 +7,7 @@ that the module refuses CPU tensors (no CPU fallback).
 GPU: forward and parameter gradients equal those of the same module whose sampling step
 is the oracle (oracle/torch_ref), run on the CPU in fp32, within 1e-4 normwise; exercised
 with query and head chunking, padding mask, positional encoding, sequence-first layout and
-checkpointing.
+checkpointing, for the fused (locations and softmax in the kernel) and unfused paths.
 """
 
 from __future__ import annotations
@@ -86,12 +86,15 @@ def _oracle_module(m):
     """A CPU copy of module m whose sampling step is the oracle."""
     r = copy.deepcopy(m).cpu()
     r._msda = lambda v, s, lo, a: torch_ref.msda_ref(v, s, lo, a, r.clamp_grid, r.clamp_eps)
+    r._msda_fused = lambda v, s, rf, o, lg: torch_ref.msda_fused_ref(v, s, rf, o, lg, r.clamp_grid,
+                                                                     r.clamp_eps)
     return r
 
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("dim", [2, 3])
-def test_module_matches_oracle_module(dim):
+@pytest.mark.parametrize("fused", [True, False])
+def test_module_matches_oracle_module(dim, fused):
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     torch.manual_seed(0)
@@ -100,14 +103,14 @@ def test_module_matches_oracle_module(dim):
     nv = int(shapes.prod(-1).sum())
     E, H, nq, bs = 64, 4, 37, 2
     m = cls(E, num_heads=H, num_levels=2, num_points=3, dropout=0.0, query_chunk_size=16,
-            head_chunk_size=3, use_checkpoint=True)
+            head_chunk_size=3, use_checkpoint=True, fused=fused)
     m.init_weights()
     with torch.no_grad():  # non-trivial offsets and weights
         m.sampling_offsets.weight.normal_(0, 0.05)
         m.attention_weights.weight.normal_(0, 0.2)
     m.train()
     ref = _oracle_module(m)
-    print(f"module parity dim={dim}", flush=True)
+    print(f"module parity dim={dim} fused={fused}", flush=True)
     g = torch.Generator().manual_seed(1)
     query = torch.randn(nq, bs, E, generator=g)          # sequence-first (batch_first=False)
     value = torch.randn(nv, bs, E, generator=g)
