@@ -8,13 +8,15 @@ The 3D 4-level workload (configs[4], bf16, 10% of points within 1e-3 of a volume
 timed in the same run and reported under "also".
 
 value = algorithmic bytes of fwd+bwd per step / step time, in GB/s, with inputs resident in
-HBM. Algorithmic bytes, s = element size (SURVEY 8d): V = B*K*H*C*s, G = B*Q*H*L*P*2^d*C*s,
+HBM. Algorithmic bytes, s = element size: V = B*K*H*C*s, G = B*Q*H*L*P*2^d*C*s,
 S = B*Q*H*L*P*d*s, A = B*Q*H*L*P*s, O = B*Q*H*C*s, V' = min(V, G);
 fwd = V' + S + A + O, bwd = 2V' + 2S + 2A + O.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
        python bench.py --mode copy   (plain copy kernel of known size, for PMC calibration)
        python bench.py --mode fwd|bwd --config c2|c5 (one entry only, for rocprofv3)
+       python bench.py --mode fused --config c2|c5 (producer-fused op against the modules'
+                                                    order of operations)
 """
 
 from __future__ import annotations
@@ -39,7 +41,7 @@ METRIC = "MSDA fwd & fwd+bwd ms + achieved HBM GB/s, 2D encoder & 3D 4-level, bf
 HBM_PEAK_GBPS = 8000.0
 # kernels behind the roofline objects (the C2 bf16 launch: 2D, bf16 value and coordinates,
 # 8 channels per lane, 4 points per coordinate block, quad-shared geometry)
-FWD_KERNEL = "msda::msda_fwd_staged_kernel<2, msda::BF16, msda::BF16, 8, 4, true>"
+FWD_KERNEL = "msda::msda_fwd_staged_kernel<2, msda::BF16, msda::BF16, 8, 4, true, false>"
 BWD_KERNELS = ("msda_bwd entry: bwd_grad_kernel, bwd_colscan_kernel, bwd_plan_kernel, "
                "bwd_fill_kernel, bwd_tile_kernel, bwd_fold_kernel and workspace clears")
 
@@ -195,6 +197,63 @@ def measure_case(cfg, device, steps, warmup):
     }
 
 
+def measure_fused(cfg, device, steps, warmup):
+    """The producer-fused op (msda2d_fused / msda3d_fused: locations and softmax weights
+    formed in the kernel) against the attention modules' order of operations (softmax over
+    L*P, reference + offset / normaliser, then the plain op), forward and fwd+bwd."""
+    import msda_triton
+    from msda_triton.hip import _core, fused
+
+    g = torch.Generator().manual_seed(5)
+    d, B, H, C, P = cfg["dim"], cfg["B"], cfg["H"], cfg["C"], cfg["P"]
+    L, Q, K = len(cfg["shapes"]), cfg["Q"], num_keys(cfg)
+    dt = DTYPES[cfg["dtype"]]
+    shapes = torch.tensor(cfg["shapes"], dtype=torch.int64)
+    value = torch.randn(B, K, H, C, generator=g).to(device, dt)
+    ref = torch.rand(B, Q, L, d, generator=g).to(device)
+    off = (2.0 * torch.randn(B, Q, H, L, P, d, generator=g)).to(device, dt)  # pixels
+    logits = torch.randn(B, Q, H, L, P, generator=g).to(device, dt)
+    grad_out = torch.randn(B, Q, H * C, generator=g).to(device, dt)
+    norm = shapes.flip(-1).to(device)
+    levels = _core.prepare_levels(d, value, shapes)
+    op_f = msda_triton.msda2d_fused if d == 2 else msda_triton.msda3d_fused
+    op_p = msda_triton.msda2d if d == 2 else msda_triton.msda3d
+
+    def form(o, lg, r):
+        attn = lg.view(B, Q, H, L * P).softmax(-1).view(B, Q, H, L, P)
+        return r[:, :, None, :, None, :] + o / norm[None, None, None, :, None, :], attn
+
+    def fwd_fused():
+        return fused.forward(d, value, levels, ref, off, logits, True, 1e-4)[0]
+
+    def fwd_unfused():
+        loc, attn = form(off, logits, ref)
+        return _core.forward(d, value, levels, loc.to(dt), attn, True, 1e-4)[0]
+
+    def leaves():
+        return (value.detach().requires_grad_(True), ref.detach().requires_grad_(True),
+                off.detach().requires_grad_(True), logits.detach().requires_grad_(True))
+
+    def step_fused():
+        v, r, o, lg = leaves()
+        op_f(v, shapes, r, o, lg).backward(grad_out)
+
+    def step_unfused():
+        v, r, o, lg = leaves()
+        loc, attn = form(o, lg, r)
+        op_p(v, shapes, loc.to(dt), attn).backward(grad_out)
+
+    n = max(steps, 20)
+    return {"fwd_ms": round(time_events(fwd_fused, n, warmup), 5),
+            "unfused_fwd_ms": round(time_events(fwd_unfused, n, warmup), 5),
+            "fwd_bwd_ms": round(time_events(step_fused, n, warmup), 5),
+            "unfused_fwd_bwd_ms": round(time_events(step_unfused, n, warmup), 5),
+            "note": "fused: msda*_fused (reference points, pixel offsets and logits in; "
+                    "locations and softmax formed in the kernel); unfused: the modules' torch "
+                    "softmax and location formation, then msda*; fwd_bwd with gradients for "
+                    "value, reference points, offsets and logits"}
+
+
 def cpu_baseline(cfg, q_sample=None, reps=3):
     """The oracle (torch grid_sample restatement, fp32 on upcast inputs) timed on the host
     CPU: fwd + backward of out.sum(), on the first q_sample queries of the workload."""
@@ -249,7 +308,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--mode", choices=["full", "fwd", "bwd", "step", "copy"], default="full")
+    ap.add_argument("--mode", choices=["full", "fwd", "bwd", "step", "copy", "fused"], default="full")
     ap.add_argument("--config", choices=sorted(CONFIGS), default="c2")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-queries", type=int, default=None)
@@ -257,7 +316,7 @@ def main():
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(MSDA shards by (batch, head) with no exchange; see DESIGN.md). Use --gpus 1.",
+              "(MSDA shards by (batch, head) with no exchange between shards). Use --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
@@ -272,6 +331,10 @@ def main():
         dst = torch.empty_like(src)
         ms = time_events(lambda: dst.copy_(src), args.steps, args.warmup)
         print(json.dumps({"mode": "copy", "bytes_read": n, "bytes_written": n, "ms": ms}))
+        return
+    if args.mode == "fused":
+        r = measure_fused(CONFIGS[args.config], device, args.steps, args.warmup)
+        print(json.dumps({"mode": "fused", "config": args.config, **r}))
         return
     if args.mode in ("fwd", "bwd", "step"):
         case = GpuCase(CONFIGS[args.config], device)
@@ -292,6 +355,8 @@ def main():
     import msda_triton
     c3_args = (c3.value, c3.shapes, c3.loc, c3.attn)
     c3_fwd_ms = time_events(lambda: msda_triton.msda2d_fwd(*c3_args), max(args.steps, 20), args.warmup)
+    fused_c2 = measure_fused(main_cfg, device, args.steps, args.warmup)
+    fused_c5 = measure_fused(also_cfg, device, args.steps, args.warmup)
 
     # roofline: the forward kernel, which is one launch per msda2d_fwd call (the kernel the
     # bf16 forward target is stated on); the backward entry (sample-gradient, record fill,
@@ -339,7 +404,9 @@ def main():
         "also": {"c5_bf16_3d_4level": summary(r5),
                  **{k: summary(v) for k, v in extra.items()},
                  "c3_bf16_decoder": {"fwd_ms": round(c3_fwd_ms, 5),
-                                     "note": "msda2d_fwd through the Python API (host time included)"}},
+                                     "note": "msda2d_fwd through the Python API (host time included)"},
+                 "c2_bf16_fused_producer": fused_c2,
+                 "c5_bf16_fused_producer": fused_c5},
         "roofline": roofline,
         "roofline_bwd": roofline_bwd,
         "cpu_baseline": cpu,

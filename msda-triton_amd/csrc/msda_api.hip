@@ -512,6 +512,12 @@ int run_fused_kernels(const msda_desc* d, const int32_t* hs, msda::FusedArgs a, 
   a.H = d->num_heads;
   a.L = d->num_levels;
   a.P = d->num_points;
+  const int64_t lp = (int64_t)d->num_levels * d->num_points;
+  a.g_log2 = -1;
+  if (lp <= 64) {
+    a.g_log2 = 0;
+    while ((1 << a.g_log2) < lp) ++a.g_log2;
+  }
   const int64_t nb = batches_per_launch(d, lay);
   const int sc = elem_bytes(d->coord_dtype);
   const uint64_t LP = (uint64_t)d->num_levels * d->num_points;

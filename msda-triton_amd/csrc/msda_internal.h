@@ -195,6 +195,7 @@ struct FusedArgs {
   uint32_t units;           // Bc * Q * H
   uint32_t bq;              // Bc * Q
   int32_t H, L, P;
+  int32_t g_log2;           // lanes per unit = 2^g_log2 >= L * P (<= 64), or -1: one thread per unit
   float inv[kMaxLevels][3];   // 1/W, 1/H, 1/D per level (fp32, correctly rounded)
 };
 
