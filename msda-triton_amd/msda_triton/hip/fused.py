@@ -169,33 +169,46 @@ def fused_forward_only(dim, value, value_spatial_shapes, reference_points, sampl
     return out
 
 
+def _fused(dim, value, shapes, ref, off, logits, clamp_grid, clamp_eps):
+    if torch.compiler.is_compiling():  # an opaque custom op instead of a graph break
+        from . import ops
+        return ops.msda_fwd_fused(value, shapes, ref, off, logits, dim, clamp_grid, clamp_eps)
+    return MSDAFusedFn.apply(dim, value, shapes, ref, off, logits, clamp_grid, clamp_eps)
+
+
+def _fused_fwd(dim, value, shapes, ref, off, logits, clamp_grid, clamp_eps):
+    with torch.no_grad():
+        if torch.compiler.is_compiling():
+            from . import ops
+            return ops.msda_fwd_fused(value, shapes, ref, off, logits, dim, clamp_grid, clamp_eps)
+        return fused_forward_only(dim, value, shapes, ref, off, logits, clamp_grid, clamp_eps)
+
+
 def msda2d_fused(value, value_spatial_shapes, reference_points, sampling_offsets,
                  attention_logits, clamp_grid: bool = True, clamp_eps: float = 1e-4):
     """2D MSDA with location and weight formation in the kernel (see the module docstring).
     Differentiable with respect to value, reference_points, sampling_offsets and
     attention_logits. Returns (B, Q, H*C) in value's dtype."""
-    return MSDAFusedFn.apply(2, value, value_spatial_shapes, reference_points, sampling_offsets,
-                             attention_logits, clamp_grid, clamp_eps)
+    return _fused(2, value, value_spatial_shapes, reference_points, sampling_offsets,
+                  attention_logits, clamp_grid, clamp_eps)
 
 
 def msda3d_fused(value, value_spatial_shapes, reference_points, sampling_offsets,
                  attention_logits, clamp_grid: bool = True, clamp_eps: float = 1e-4):
     """3D counterpart of msda2d_fused; spatial shapes are (D, H, W) per level."""
-    return MSDAFusedFn.apply(3, value, value_spatial_shapes, reference_points, sampling_offsets,
-                             attention_logits, clamp_grid, clamp_eps)
+    return _fused(3, value, value_spatial_shapes, reference_points, sampling_offsets,
+                  attention_logits, clamp_grid, clamp_eps)
 
 
 def msda2d_fused_fwd(value, value_spatial_shapes, reference_points, sampling_offsets,
                      attention_logits, clamp_grid: bool = True, clamp_eps: float = 1e-4):
     """Forward-only msda2d_fused (no autograd graph), like msda2d_fwd."""
-    with torch.no_grad():
-        return fused_forward_only(2, value, value_spatial_shapes, reference_points,
-                                  sampling_offsets, attention_logits, clamp_grid, clamp_eps)
+    return _fused_fwd(2, value, value_spatial_shapes, reference_points, sampling_offsets,
+                      attention_logits, clamp_grid, clamp_eps)
 
 
 def msda3d_fused_fwd(value, value_spatial_shapes, reference_points, sampling_offsets,
                      attention_logits, clamp_grid: bool = True, clamp_eps: float = 1e-4):
     """Forward-only msda3d_fused."""
-    with torch.no_grad():
-        return fused_forward_only(3, value, value_spatial_shapes, reference_points,
-                                  sampling_offsets, attention_logits, clamp_grid, clamp_eps)
+    return _fused_fwd(3, value, value_spatial_shapes, reference_points, sampling_offsets,
+                      attention_logits, clamp_grid, clamp_eps)

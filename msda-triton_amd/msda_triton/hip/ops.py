@@ -8,10 +8,16 @@ node with a shape function instead:
   msda_triton::msda_bwd(grad_out, value, spatial_shapes, loc, attn, dim, clamp_grid,
                         clamp_eps) -> (grad_value, grad_loc, grad_attn)
 
-msda_fwd is differentiable through msda_bwd. Both run the same host code and kernels as the
-eager entry points (validation, level tables, C ABI), and return fresh tensors in the
-input dtypes. The public functions use them only while compiling; eager calls keep the
-autograd.Function path of the reference's API.
+  msda_triton::msda_fwd_fused(value, spatial_shapes, reference_points, sampling_offsets,
+                              attention_logits, dim, clamp_grid, clamp_eps) -> out
+  msda_triton::msda_bwd_fused(grad_out, value, spatial_shapes, reference_points,
+                              sampling_offsets, attention_logits, dim, clamp_grid,
+                              clamp_eps) -> (grad_value, grad_ref, grad_off, grad_logits)
+
+msda_fwd (msda_fwd_fused) is differentiable through msda_bwd (msda_bwd_fused). They run the
+same host code and kernels as the eager entry points (validation, level tables, C ABI),
+and return fresh tensors in the input dtypes. The public functions use them only while
+compiling; eager calls keep the autograd.Function paths.
 """
 
 from __future__ import annotations
@@ -19,7 +25,7 @@ from __future__ import annotations
 import torch
 from torch import Tensor
 
-from . import _core
+from . import _core, fused
 
 _NAMES = {2: "MSDA2D", 3: "MSDA3D"}
 
@@ -75,3 +81,65 @@ def _backward(ctx, grad_output):
 
 
 msda_fwd.register_autograd(_backward, setup_context=_setup_context)
+
+
+@torch.library.custom_op("msda_triton::msda_fwd_fused", mutates_args=())
+def msda_fwd_fused(value: Tensor, value_spatial_shapes: Tensor, reference_points: Tensor,
+                   sampling_offsets: Tensor, attention_logits: Tensor, dim: int, clamp_grid: bool,
+                   clamp_eps: float) -> Tensor:
+    return fused.fused_forward_only(dim, value, value_spatial_shapes, reference_points,
+                                    sampling_offsets, attention_logits, clamp_grid, clamp_eps)
+
+
+@msda_fwd_fused.register_fake
+def _msda_fwd_fused_fake(value, value_spatial_shapes, reference_points, sampling_offsets,
+                         attention_logits, dim, clamp_grid, clamp_eps):
+    bsz, _, num_heads, ch = value.shape
+    return value.new_empty((bsz, sampling_offsets.shape[1], num_heads * ch))
+
+
+@torch.library.custom_op("msda_triton::msda_bwd_fused", mutates_args=())
+def msda_bwd_fused(grad_output: Tensor, value: Tensor, value_spatial_shapes: Tensor,
+                   reference_points: Tensor, sampling_offsets: Tensor, attention_logits: Tensor,
+                   dim: int, clamp_grid: bool, clamp_eps: float
+                   ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    logits, ref = fused.validate_fused_inputs(fused._NAMES[dim], dim, value, value_spatial_shapes,
+                                              reference_points, sampling_offsets, attention_logits)
+    levels = _core.prepare_levels(dim, value, value_spatial_shapes)
+    cdt = _core.coord_dtype(value, sampling_offsets, logits)
+    value_c = _core._aligned(value.contiguous())
+    ref_c = ref.to(dtype=torch.float32).contiguous()
+    off_c = _core._aligned(sampling_offsets.to(dtype=cdt).contiguous())
+    logits_c = _core._aligned(logits.to(dtype=cdt).contiguous())
+    gv, gr, go, gl = fused.backward(dim, grad_output, value_c, levels, ref_c, off_c, logits_c,
+                                    clamp_grid, clamp_eps)
+    if reference_points.shape[2] == 1 and gr.shape[2] != 1:
+        gr = gr.sum(dim=2, keepdim=True)
+    return (gv.to(value.dtype), gr.to(reference_points.dtype), go.to(sampling_offsets.dtype),
+            gl.to(attention_logits.dtype).reshape(attention_logits.shape))
+
+
+@msda_bwd_fused.register_fake
+def _msda_bwd_fused_fake(grad_output, value, value_spatial_shapes, reference_points,
+                         sampling_offsets, attention_logits, dim, clamp_grid, clamp_eps):
+    cf = torch.contiguous_format
+    return (torch.empty_like(value, memory_format=cf),
+            torch.empty_like(reference_points, memory_format=cf),
+            torch.empty_like(sampling_offsets, memory_format=cf),
+            torch.empty_like(attention_logits, memory_format=cf))
+
+
+def _setup_context_fused(ctx, inputs, output):
+    value, shapes, ref, off, logits, dim, clamp_grid, clamp_eps = inputs
+    ctx.save_for_backward(value, shapes, ref, off, logits)
+    ctx.dim, ctx.clamp_grid, ctx.clamp_eps = dim, clamp_grid, clamp_eps
+
+
+def _backward_fused(ctx, grad_output):
+    value, shapes, ref, off, logits = ctx.saved_tensors
+    gv, gr, go, gl = msda_bwd_fused(grad_output.contiguous(), value, shapes, ref, off, logits,
+                                    ctx.dim, ctx.clamp_grid, ctx.clamp_eps)
+    return gv, None, gr, go, gl, None, None, None
+
+
+msda_fwd_fused.register_autograd(_backward_fused, setup_context=_setup_context_fused)
