@@ -63,7 +63,7 @@ __device__ inline uint32_t block_excl_scan(uint32_t v, uint32_t* s_w, uint32_t* 
   const uint32_t inc = wave_incl_scan(v);
   const int w = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
   if (lane == kWave - 1) s_w[w] = inc;
-  __syncthreads();
+  lds_sync();
   uint32_t pre = 0, tot = 0;
 #pragma unroll
   for (int i = 0; i < NT / kWave; ++i) {
@@ -71,7 +71,7 @@ __device__ inline uint32_t block_excl_scan(uint32_t v, uint32_t* s_w, uint32_t* 
     if (i < w) pre += x;
     tot += x;
   }
-  __syncthreads();
+  lds_sync();
   *total = tot;
   return pre + inc - v;
 }
@@ -135,16 +135,16 @@ __device__ inline BinUnit bin_unit(const BwdPlan& pl, uint32_t g, uint32_t w, ui
   return bu;
 }
 
-// Pixel coordinates, clamp flags and anchor tile of one sample; false if the sample has
-// no corner inside its level.
-template <int DIM, typename TC>
-__device__ inline bool sample_tile(const BwdPlan& pl, const BwdLevel& lv, const TC* lp, float* u,
+// Pixel coordinates, clamp flags and anchor tile of one sample at location xyz; false if
+// the sample has no corner inside its level.
+template <int DIM>
+__device__ inline bool sample_tile(const BwdPlan& pl, const BwdLevel& lv, const float* xyz, float* u,
                                    uint32_t* flags, int* tib) {
   bool px, py, pz = true;
-  u[0] = grid_to_u((float)lp[0], (float)lv.W, pl.clamp, pl.lo_g, pl.hi_g, &px);
-  u[1] = grid_to_u((float)lp[1], (float)lv.H, pl.clamp, pl.lo_g, pl.hi_g, &py);
+  u[0] = grid_to_u(xyz[0], (float)lv.W, pl.clamp, pl.lo_g, pl.hi_g, &px);
+  u[1] = grid_to_u(xyz[1], (float)lv.H, pl.clamp, pl.lo_g, pl.hi_g, &py);
   u[2] = 0.0f;
-  if constexpr (DIM == 3) u[2] = grid_to_u((float)lp[2], (float)lv.D, pl.clamp, pl.lo_g, pl.hi_g, &pz);
+  if constexpr (DIM == 3) u[2] = grid_to_u(xyz[2], (float)lv.D, pl.clamp, pl.lo_g, pl.hi_g, &pz);
   const Axis ax = axis_from_u(u[0], lv.W, px);
   const Axis ay = axis_from_u(u[1], lv.H, py);
   const Axis az = DIM == 3 ? axis_from_u(u[2], lv.D, pz) : Axis{1.0f, 0.0f, 0, true, false, true};
@@ -456,32 +456,45 @@ __global__ __launch_bounds__(kBlock) void bwd_fill_kernel(const BwdPlan pl, cons
     for (uint32_t r0 = 0; r0 < n; r0 += kFillStage) {
       const uint32_t nr = min((uint32_t)kFillStage, n - r0);
       for (uint32_t i = lb0 + threadIdx.x; i < lb1; i += kBlock) s_cnt[i] = 0;
-      __syncthreads();
-      // rank each sample of the round within its bin; its record stays in registers
+      lds_sync();
+      // every coordinate and weight load of the round first (no branch between them, so
+      // they are in flight together), then rank each sample within its bin; its record
+      // stays in registers. (Prefetching the next round's loads here was slower.)
       uint32_t key[KP];
       uint32_t rw[KP][RW];
+      float xyz[KP][DIM], at[KP];
+      uint32_t qp[KP], hs[KP];
 #pragma unroll
       for (int k = 0; k < KP; ++k) {
-        key[k] = 0xffffffffu;
         const uint32_t j = threadIdx.x + k * kBlock;
-        if (j >= nr) continue;
-        const uint32_t js = r0 + j;
+        const uint32_t js = r0 + (j < nr ? j : 0u);
         const uint32_t wi = fdiv(js, pl.div_p), p = js - wi * (uint32_t)pl.P;
         const BinUnit bu = bin_unit(pl, g, w, wi);
         const size_t si = bu.bqh * LP + (size_t)l * pl.P + p;
+        const TC* lp = static_cast<const TC*>(bf.loc) + si * DIM;
+#pragma unroll
+        for (int d = 0; d < DIM; ++d) xyz[k][d] = (float)lp[d];
+        at[k] = (float)static_cast<const TC*>(bf.attn)[si];
+        qp[k] = bu.q * (uint32_t)pl.P + p;
+        hs[k] = bu.hsub;
+      }
+#pragma unroll
+      for (int k = 0; k < KP; ++k) {
+        key[k] = 0xffffffffu;
+        if (threadIdx.x + k * kBlock >= nr) continue;
         float u[3];
         uint32_t flags;
         int tib;
-        if (!sample_tile<DIM>(pl, lv, static_cast<const TC*>(bf.loc) + si * DIM, u, &flags, &tib)) continue;
-        const uint32_t bin = ((uint32_t)tib << pl.hg_log2) | bu.hsub;
+        if (!sample_tile<DIM>(pl, lv, xyz[k], u, &flags, &tib)) continue;
+        const uint32_t bin = ((uint32_t)tib << pl.hg_log2) | hs[k];
         key[k] = (bin << 16) | atomicAdd(&s_cnt[bin], 1u);
-        rw[k][0] = (bu.q * (uint32_t)pl.P + p) | flags;
+        rw[k][0] = qp[k] | flags;
         rw[k][1] = as_u32(u[0]);
         rw[k][2] = as_u32(u[1]);
         if constexpr (DIM == 3) rw[k][3] = as_u32(u[2]);
-        rw[k][RW - 1] = as_u32((float)static_cast<const TC*>(bf.attn)[si]);
+        rw[k][RW - 1] = as_u32(at[k]);
       }
-      __syncthreads();
+      lds_sync();
       // exclusive scan of the round's counts over the level's bins
       uint32_t carry = 0;
       for (uint32_t b0 = lb0; b0 < lb1; b0 += kBlock) {
@@ -492,7 +505,7 @@ __global__ __launch_bounds__(kBlock) void bwd_fill_kernel(const BwdPlan pl, cons
         if (i < lb1) s_cnt[i] = carry + ex;
         carry += tot;
       }
-      __syncthreads();
+      lds_sync();
       // place the records sorted by bin
 #pragma unroll
       for (int k = 0; k < KP; ++k) {
@@ -503,7 +516,7 @@ __global__ __launch_bounds__(kBlock) void bwd_fill_kernel(const BwdPlan pl, cons
         for (int i = 0; i < RW; ++i) rec[i] = rw[k][i];
         s_dst[pos] = s_base[bin] + rank;
       }
-      __syncthreads();
+      lds_sync();
       // copy out: consecutive threads write consecutive records of a bin; four words per
       // thread and step, so their LDS reads overlap
       {
@@ -525,11 +538,11 @@ __global__ __launch_bounds__(kBlock) void bwd_fill_kernel(const BwdPlan pl, cons
             if (d[u] != 0xffffffffu) bf.records[d[u]] = v[u];
         }
       }
-      __syncthreads();
+      lds_sync();
       // advance the bins' global positions by the round's counts
       for (uint32_t i = lb0 + threadIdx.x; i < lb1; i += kBlock)
         s_base[i] += (i + 1 < lb1 ? s_cnt[i + 1] : carry) - s_cnt[i];
-      __syncthreads();  // the next round clears s_cnt
+      lds_sync();  // the next round clears s_cnt
     }
   }
 }
@@ -654,7 +667,7 @@ __global__ __launch_bounds__(kTileThreads, kTileWavesPerSimd) void bwd_tile_kern
 #pragma unroll
     for (int k = 0; k < RW; ++k) rec[k] = bf.records[(size_t)(beg + tid) * RW + k];
   }
-  __syncthreads();
+  lds_sync();
 
   int par = 0;
   for (uint32_t sb = beg; sb < end; sb += S, par ^= 1) {
@@ -711,7 +724,7 @@ __global__ __launch_bounds__(kTileThreads, kTileWavesPerSimd) void bwd_tile_kern
         }
       }
     }
-    __syncthreads();
+    lds_sync();
 
     // 2. scan this set of counters; clear the other (last read in the previous sub-batch)
     if (wv == 0) wave_scan_counts(s_cnt, ncell_r);
@@ -719,7 +732,7 @@ __global__ __launch_bounds__(kTileThreads, kTileWavesPerSimd) void bwd_tile_kern
       uint32_t* o = s_cnt2 + (par ^ 1) * (ncell_r + 1);
       for (int i = tid; i <= ncell_r; i += NT) o[i] = 0u;
     }
-    __syncthreads();
+    lds_sync();
 
     // 3. place the entries; fetch the next sub-batch's record
     if (has) {
@@ -739,7 +752,7 @@ __global__ __launch_bounds__(kTileThreads, kTileWavesPerSimd) void bwd_tile_kern
         for (int k = 0; k < RW; ++k) rec[k] = bf.records[(size_t)nx * RW + k];
       }
     }
-    __syncthreads();
+    lds_sync();
 
     // 4. owner pass: fp32 register accumulation per (region cell, channel chunk)
 #pragma unroll
@@ -773,7 +786,7 @@ __global__ __launch_bounds__(kTileThreads, kTileWavesPerSimd) void bwd_tile_kern
         }
       }
     }
-    __syncthreads();  // LDS of this sub-batch is reused by the next one
+    lds_sync();  // LDS of this sub-batch is reused by the next one
   }
 
   // write the region: interior cells of a one-chunk tile directly in the value dtype;

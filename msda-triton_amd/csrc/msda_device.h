@@ -25,6 +25,16 @@ struct FastDiv {
   uint32_t d, m, s;
 };
 
+// Workgroup barrier that orders LDS only: waits for this wave's LDS operations, not for
+// its outstanding global loads (which __syncthreads' workgroup fence also waits for), so
+// loads issued before it stay in flight across it. For phases that share data through
+// LDS alone.
+__device__ inline void lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __host__ __device__ inline FastDiv make_fastdiv(uint32_t d) {
   FastDiv f;
   f.d = d;
