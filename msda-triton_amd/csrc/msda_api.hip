@@ -39,7 +39,10 @@ const char* dtype_name(int dt) {
 constexpr uint64_t kLim31 = 0x7FFFFFFFull;
 constexpr uint64_t kCus = 256;  // MI355X compute units: workgroups of the staged forward
 constexpr uint32_t kChunkRecords = 4096;        // records per tile-kernel chunk (rounded to S)
-constexpr uint32_t kTileLdsTarget = 80 * 1024 - 256;  // two tile workgroups per CU (160 KB LDS)
+// LDS share of one tile workgroup at the kernel's occupancy target (160 KB LDS per CU):
+// four workgroups in 2D, two in 3D
+constexpr uint32_t kTileLdsTarget2 = 40 * 1024 - 256;
+constexpr uint32_t kTileLdsTarget3 = 80 * 1024 - 256;
 constexpr uint32_t kTileLdsBudget = 160 * 1024 - 256;  // one workgroup per CU
 constexpr int kMaxBinsLds = 8192;  // bin histogram + bases in 64 KB of LDS
 constexpr uint64_t kL2Bytes = 4ull << 20;  // L2 of one XCD
@@ -231,12 +234,12 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
                 "backward supports Q*P up to 2^27 per launch, got Q=%lld P=%d",
                 (long long)d->num_queries, d->num_points);
   // Tile extents and sub-batch size: start from 16x16 (2D) / 8x8x8 (3D) cells and
-  // S = kTileThreads records (one per thread); halve the largest tile extent until a thread
+  // S = kTileThreads<dim> records (one per thread); halve the largest tile extent until a thread
   // owns at most kTileMaxItems (region cell, owner chunk) items, and lower S in steps of
   // one wave until the sub-batch's fp32 grad_out rows, sorted entries and two counter sets
-  // fit the LDS share of one of two workgroups per CU (or, for very wide heads, all of a
+  // fit the LDS share of one workgroup at the occupancy target (or, for very wide heads, all of a
   // CU's LDS).
-  const uint32_t NT = msda::kTileThreads;
+  const uint32_t NT = d->dim == 2 ? msda::kTileThreads<2> : msda::kTileThreads<3>;
   const uint32_t grow = (uint32_t)d->channels * 4u;
   const int onv = d->channels / msda::tile_owner_vec(lay.vec_bytes / s);
   int T[3];
@@ -277,7 +280,7 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
       S = NT;
     }
   };
-  if (!fit(kTileLdsTarget) && !fit(kTileLdsBudget))
+  if (!fit(d->dim == 2 ? kTileLdsTarget2 : kTileLdsTarget3) && !fit(kTileLdsBudget))
     return fail(MSDA_ERR_INVALID, "channels per head (%d) too large for the backward", d->channels);
   pl.TX = T[0];
   pl.TY = T[1];

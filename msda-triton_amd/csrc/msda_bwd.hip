@@ -598,8 +598,8 @@ __device__ inline void wave_scan_counts(uint32_t* c, int n) {
   if (lane == kWave - 1) c[n] = inc;
 }
 
-// One workgroup (kTileThreads threads) per chunk of a tile's records, in sub-batches of
-// S <= kTileThreads records; thread t owns record t of the sub-batch in registers. LDS
+// One workgroup (kTileThreads<DIM> threads) per chunk of a tile's records, in sub-batches of
+// S <= kTileThreads<DIM> records; thread t owns record t of the sub-batch in registers. LDS
 // holds the sub-batch's grad_out rows widened to fp32, its (attn * corner weight, row
 // byte offset) entries sorted by region cell, and two sets of per-cell counters (one
 // being filled while the other is cleared). Per sub-batch, four barriers:
@@ -611,9 +611,9 @@ __device__ inline void wave_scan_counts(uint32_t* c, int n) {
 //   4. the thread owning (region cell, channel chunk) sums its cell's entries into fp32
 //      registers.
 template <int DIM, typename EV, typename EC, int VEC>
-__global__ __launch_bounds__(kTileThreads, kTileWavesPerSimd) void bwd_tile_kernel(const BwdPlan pl,
+__global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile_kernel(const BwdPlan pl,
                                                                 const BwdBuffers bf) {
-  constexpr int NT = kTileThreads;
+  constexpr int NT = kTileThreads<DIM>;
   constexpr int VB = VEC * EV::kBytes;
   constexpr int NC = 1 << DIM;
   constexpr int RW = DIM + 2;        // words per record
@@ -920,7 +920,7 @@ hipError_t run_bwd_t(const BwdPlan& pl, const BwdBuffers& bf, hipStream_t s) {
                             (kBlock / kWave) * sizeof(uint32_t);
   hipLaunchKernelGGL((bwd_fill_kernel<DIM, EC>), dim3(nbin_wg), dim3(kBlock), fill_bytes, s, pl, bf);
   hipLaunchKernelGGL((bwd_tile_kernel<DIM, EV, EC, VEC>), dim3(pl.grid_chunks),
-                     dim3(kTileThreads), pl.lds_bytes, s, pl, bf);
+                     dim3(kTileThreads<DIM>), pl.lds_bytes, s, pl, bf);
   hipLaunchKernelGGL((bwd_fold_kernel<DIM, EV, VEC>), dim3(pl.T), dim3(kBlock), 0, s, pl, bf);
   return hipGetLastError();
 }

@@ -9,13 +9,17 @@
 namespace msda {
 
 constexpr int kMaxLevels = 64;
-constexpr int kTileThreads = 512;     // threads of the backward tile kernel (8 waves)
+// threads of the backward tile kernel: 2D 256 (four workgroups per CU, 16x8-cell tiles),
+// 3D 512 (two workgroups per CU: smaller workgroups would shrink the 3D tiles to 4x4x4 and
+// double the bins and the fill's work)
+template <int DIM>
+constexpr int kTileThreads = DIM == 2 ? 256 : 512;
 // (region cell, 4-channel chunk) owner items per tile thread
 template <int DIM>
 constexpr int kTileMaxItems = 5;
 // channels per owner item of the tile kernel for VEC channels per value load
 constexpr int tile_owner_vec(int vec) { return vec < 4 ? vec : 4; }
-constexpr int kTileWavesPerSimd = 4;  // tile-kernel occupancy target: two workgroups per CU
+constexpr int kTileWavesPerSimd = 4;  // tile-kernel occupancy target (128 VGPRs)
 constexpr int kFillStage = 2048;      // records staged in LDS per fill round
 constexpr int kGradThreads = 256;     // threads of the backward sample-gradient kernel
 constexpr int kGradRounds = 4;        // unit groups each of its threads handles in turn
@@ -129,7 +133,7 @@ struct BwdPlan {
   int32_t bins;                // tiles_per_bh * HG; bin = tile_in_bh * HG + head_in_group
   uint32_t T;                  // groups * bins: tiles of this launch
   uint32_t R;                  // records per chunk (multiple of S)
-  uint32_t S;                  // records per LDS sub-batch of the tile kernel (<= kTileThreads)
+  uint32_t S;                  // records per LDS sub-batch of the tile kernel (<= kTileThreads<DIM>)
   int32_t lpu_log2, nvec;
   int32_t clamp;
   int32_t coords_aligned;      // loc and attn are 16-byte aligned: per-batch block loads allowed
