@@ -436,12 +436,12 @@ __global__ __launch_bounds__(kBlock) void bwd_fill_kernel(const BwdPlan pl, cons
   typedef typename EC::T TC;
   constexpr int RW = DIM + 2;
   constexpr int KP = kFillStage / kBlock;  // samples per thread per round
-  extern __shared__ uint32_t s_fill[];
-  uint32_t* s_base = s_fill;               // [bins] next global record of each bin
-  uint32_t* s_cnt = s_base + pl.bins;      // [bins] round counts -> round offsets
-  uint32_t* s_rec = s_cnt + pl.bins;       // [kFillStage * RW] records sorted by bin
+  extern __shared__ __attribute__((aligned(16))) uint32_t s_fill[];
+  uint32_t* s_rec = s_fill;                // [kFillStage * RW] records sorted by bin (16-byte aligned)
   uint32_t* s_dst = s_rec + kFillStage * RW;  // [kFillStage] global record index of each
-  uint32_t* s_w = s_dst + kFillStage;      // [kBlock / kWave]
+  uint32_t* s_base = s_dst + kFillStage;   // [bins] next global record of each bin
+  uint32_t* s_cnt = s_base + pl.bins;      // [bins] round counts -> round offsets
+  uint32_t* s_w = s_cnt + pl.bins;         // [kBlock / kWave]
   const uint32_t g = blockIdx.x / (uint32_t)pl.wgpg;
   const uint32_t w = blockIdx.x - g * (uint32_t)pl.wgpg;
   for (int i = threadIdx.x; i < pl.bins; i += kBlock)
@@ -512,14 +512,24 @@ __global__ __launch_bounds__(kBlock) void bwd_fill_kernel(const BwdPlan pl, cons
         if (key[k] == 0xffffffffu) continue;
         const uint32_t bin = key[k] >> 16, rank = key[k] & 0xffffu, pos = s_cnt[bin] + rank;
         uint32_t* rec = s_rec + pos * RW;
+        if constexpr (RW == 4) {
+          *reinterpret_cast<uint4*>(rec) = make_uint4(rw[k][0], rw[k][1], rw[k][2], rw[k][3]);
+        } else {
 #pragma unroll
-        for (int i = 0; i < RW; ++i) rec[i] = rw[k][i];
+          for (int i = 0; i < RW; ++i) rec[i] = rw[k][i];
+        }
         s_dst[pos] = s_base[bin] + rank;
       }
       lds_sync();
-      // copy out: consecutive threads write consecutive records of a bin; four words per
-      // thread and step, so their LDS reads overlap
-      {
+      // copy out: consecutive threads write consecutive records of a bin
+      if constexpr (RW == 4) {
+        // 16-byte records: one LDS read and one 16-byte store per record
+        for (uint32_t r = threadIdx.x; r < carry; r += kBlock) {
+          const uint4 v = reinterpret_cast<const uint4*>(s_rec)[r];
+          reinterpret_cast<uint4*>(bf.records)[s_dst[r]] = v;
+        }
+      } else {
+        // four words per thread and step, so their LDS reads overlap
         const uint32_t nw = carry * RW;
         for (uint32_t i0 = threadIdx.x; i0 < nw; i0 += 4 * kBlock) {
           uint32_t v[4], d[4];
