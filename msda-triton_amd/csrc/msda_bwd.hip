@@ -529,23 +529,14 @@ __global__ __launch_bounds__(kBlock) void bwd_fill_kernel(const BwdPlan pl, cons
           reinterpret_cast<uint4*>(bf.records)[s_dst[r]] = v;
         }
       } else {
-        // four words per thread and step, so their LDS reads overlap
-        const uint32_t nw = carry * RW;
-        for (uint32_t i0 = threadIdx.x; i0 < nw; i0 += 4 * kBlock) {
-          uint32_t v[4], d[4];
+        // one record per thread: its destination is read once
+        for (uint32_t r = threadIdx.x; r < carry; r += kBlock) {
+          uint32_t v[RW];
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const uint32_t i = i0 + (uint32_t)u * kBlock;
-            d[u] = 0xffffffffu;
-            if (i < nw) {
-              const uint32_t r = i / RW, k = i - r * RW;
-              v[u] = s_rec[i];
-              d[u] = s_dst[r] * RW + k;
-            }
-          }
+          for (int i = 0; i < RW; ++i) v[i] = s_rec[r * RW + i];
+          uint32_t* d = bf.records + (size_t)s_dst[r] * RW;
 #pragma unroll
-          for (int u = 0; u < 4; ++u)
-            if (d[u] != 0xffffffffu) bf.records[d[u]] = v[u];
+          for (int i = 0; i < RW; ++i) d[i] = v[i];
         }
       }
       lds_sync();
