@@ -474,9 +474,11 @@ int fwd_impl(const msda_desc* d, const void* value, const int32_t* spatial_shape
 
 
 // Workspace of msda_bwd_fused: fp32 loc, attn, grad_loc, grad_attn, then the workspace of
-// the inner msda_bwd over those fp32 tensors (coord dtype float32).
+// the inner msda_bwd over those fp32 tensors (coord dtype float32). Byte offsets.
 struct FusedWs {
-  uint64_t loc, attn, gloc, gattn, inner, total;  // byte offsets, inner: its size
+  uint64_t loc, attn, gloc, gattn;
+  uint64_t inner, inner_bytes;  // the inner msda_bwd workspace
+  uint64_t total;
 };
 
 bool fused_ws(const msda_desc* d, const int32_t* hs, FusedWs* w) {
@@ -484,17 +486,16 @@ bool fused_ws(const msda_desc* d, const int32_t* hs, FusedWs* w) {
   msda_desc d32 = *d;
   d32.coord_dtype = MSDA_F32;
   const uint64_t samples = (uint64_t)d->batch * d->num_queries * d->num_heads * d->num_levels * d->num_points;
+  BwdHostPlan hp;
+  const void* none[1] = {nullptr};
+  if (plan_bwd(&d32, hs, none, 0, &hp)) return false;
   w->loc = 0;
   w->attn = w->loc + al(samples * d->dim * 4);
   w->gloc = w->attn + al(samples * 4);
   w->gattn = w->gloc + al(samples * d->dim * 4);
-  const uint64_t inner_off = w->gattn + al(samples * 4);
-  BwdHostPlan hp;
-  const void* none[1] = {nullptr};
-  if (plan_bwd(&d32, hs, none, 0, &hp)) return false;
-  w->inner = hp.sz.total_bytes;
-  w->total = inner_off + al(w->inner);
-  w->inner = inner_off;  // from here on: offset of the inner workspace
+  w->inner = w->gattn + al(samples * 4);
+  w->inner_bytes = hp.sz.total_bytes;
+  w->total = w->inner + al(w->inner_bytes);
   return true;
 }
 
@@ -725,7 +726,7 @@ int msda_bwd_fused(const msda_desc* d, const int32_t* host_spatial_shapes, const
   float* gloc = reinterpret_cast<float*>(ws + w.gloc);
   float* gattn = reinterpret_cast<float*>(ws + w.gattn);
   rc = msda_bwd(&d32, host_spatial_shapes, value, a.loc, a.attn, grad_output, grad_value, gloc,
-                gattn, ws + w.inner, w.total - w.inner, stream);
+                gattn, ws + w.inner, w.inner_bytes, stream);
   if (rc) return rc;
   // 3. through the location and softmax formation
   a.grad_loc = gloc;
