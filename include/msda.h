@@ -131,7 +131,9 @@ size_t msda_bwd_workspace_bytes(const msda_desc* desc, const int32_t* host_spati
  * Gradients of clamped grid coordinates are zero, matching the backward of torch.clamp.
  * grad_value is accumulated in fp32 in on-chip memory per spatial tile, so no device-wide
  * atomics are used; the order of the fp32 additions within a tile is not fixed, so its
- * low-order bits may vary between runs. `workspace` must hold
+ * low-order bits may vary between runs. Levels with more than 8192 tiles per head in total
+ * (about 1 M cells) are accumulated instead with global fp32 atomics into an fp32 copy of
+ * grad_value in the workspace, then rounded once. `workspace` must hold
  * msda_bwd_workspace_bytes() bytes, 256-byte aligned; it needs no initialisation.
  *
  * Replaces the reference's MSDA2DFn.backward body (src/msda_triton/triton/msda_2d.py:778-853,

@@ -308,9 +308,20 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
   pl.S = S;
   pl.lds_g_bytes = S * grow;
   pl.lds_bytes = lds;
+  // Levels with more than kMaxBinsLds tiles per head in total do not fit the LDS binning
+  // of the sample-gradient and fill kernels: such plans scatter grad_value with fp32
+  // atomics instead (sample-gradient kernel only, then one rounding pass).
+  int64_t all_tiles = 0;
+  for (int l = 0; l < d->num_levels; ++l) {
+    const msda::BwdLevel& lv = pl.lv[l];
+    all_tiles += (int64_t)((lv.W + pl.TX - 1) / pl.TX) * ((lv.H + pl.TY - 1) / pl.TY) *
+                 ((lv.D + pl.TZ - 1) / pl.TZ);
+  }
+  const bool atomic = all_tiles > kMaxBinsLds;
+  pl.atomic = atomic ? 1 : 0;
   // tiles of the coarsest level first: its chunks are the longest, so they start early
   int tiles = 0;
-  const bool head_major = use_head_major(d);
+  const bool head_major = !atomic && use_head_major(d);
   bool mul24 = (uint64_t)(head_major ? 1 : d->num_heads) * d->channels * s < (1u << 23);
   for (int l = d->num_levels - 1; l >= 0; --l) {
     msda::BwdLevel& lv = pl.lv[l];
@@ -330,11 +341,7 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
     lv.nty = (lv.H + pl.TY - 1) / pl.TY;
     lv.ntz = (lv.D + pl.TZ - 1) / pl.TZ;
     lv.tile_off = tiles;
-    const int64_t nt = (int64_t)lv.ntx * lv.nty * lv.ntz;
-    if (tiles + nt > kMaxBinsLds)
-      return fail(MSDA_ERR_INVALID,
-                  "backward: levels too large (%lld tiles per head; the binning supports %d)",
-                  (long long)(tiles + nt), kMaxBinsLds);
+    const int64_t nt = atomic ? 0 : (int64_t)lv.ntx * lv.nty * lv.ntz;
     lv.ntiles = (int32_t)nt;
     tiles += (int)nt;
   }
@@ -373,7 +380,7 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
   pl.T = (uint32_t)pl.groups * (uint32_t)pl.bins;
   const uint64_t samples =
       (uint64_t)nb * d->num_queries * d->num_heads * d->num_levels * d->num_points;
-  pl.max_chunks = pl.T + (uint32_t)((samples + pl.R - 1) / pl.R);
+  pl.max_chunks = atomic ? 0u : pl.T + (uint32_t)((samples + pl.R - 1) / pl.R);
   pl.grid_chunks = (pl.max_chunks + msda::kXcds - 1) / msda::kXcds * msda::kXcds;
   pl.value_bytes = (uint32_t)(nb * (uint64_t)d->num_keys * d->num_heads * d->channels * s);
   out->sz = msda::bwd_sizes(pl, samples, d->dim);

@@ -36,6 +36,9 @@
 //
 // Every grad_value element is written exactly once with a plain store, so no clearing
 // pass is needed and 16-bit values are rounded once, from fp32.
+//
+// Pyramids beyond the LDS binning (more than kMaxBinsLds tiles per head) run step 1 alone
+// with global fp32 atomics into fp32 sums in the workspace, then one rounding pass.
 #include "msda_internal.h"
 #include "msda_sample.h"
 
@@ -244,8 +247,12 @@ __device__ inline bool sample_rows(const BwdPlan& pl, const BwdLevel& lv, const 
 // coordinates and weights are one block load per lane, queued behind the previous
 // batch's corner rows, and all SB*2^DIM corner rows of a batch are in flight together.
 // LG >= 0: lanes per unit (2^LG) is a compile-time constant, else pl.lpu_log2.
-template <int DIM, typename EV, typename EC, int VEC, int PT, int LG>
+// AT (plans whose levels exceed the LDS binning; PT == 0 only): instead of counting its
+// samples per tile, each lane adds attn * w_c * grad_out of its channels to every valid
+// corner row of the fp32 (Bc, K, H, C) sums in bf.scratch with global fp32 atomics.
+template <int DIM, typename EV, typename EC, int VEC, int PT, int LG, bool AT = false>
 __global__ __launch_bounds__(kGradThreads) void bwd_grad_kernel(const BwdPlan pl, const BwdBuffers bf) {
+  static_assert(!AT || PT == 0, "the atomic scatter is built on the generic sample loop");
   constexpr int VB = VEC * EV::kBytes;
   constexpr int NC = 1 << DIM;
   constexpr int SB = PT > 0 ? (DIM == 2 ? (PT < 4 ? PT : 4) : (PT < 2 ? PT : 2)) : (DIM == 2 ? 2 : 1);
@@ -256,8 +263,10 @@ __global__ __launch_bounds__(kGradThreads) void bwd_grad_kernel(const BwdPlan pl
   const uint32_t lb = xcd_logical_block(blockIdx.x, gridDim.x);
   const uint32_t g = lb / (uint32_t)pl.wgpg;
   const uint32_t w = lb - g * (uint32_t)pl.wgpg;
-  for (int i = threadIdx.x; i < pl.bins; i += kGradThreads) s_hist[i] = 0;
-  __syncthreads();
+  if constexpr (!AT) {
+    for (int i = threadIdx.x; i < pl.bins; i += kGradThreads) s_hist[i] = 0;
+    __syncthreads();
+  }
 
   const int lg = LG >= 0 ? LG : pl.lpu_log2;
   const uint32_t lanes = 1u << lg;
@@ -324,7 +333,8 @@ __global__ __launch_bounds__(kGradThreads) void bwd_grad_kernel(const BwdPlan pl
           ga[k] = o[0];
 #pragma unroll
           for (int d = 0; d < DIM; ++d) gl[k * DIM + d] = o[1 + d];
-          if (any[k] && lane == ((uint32_t)k & (lanes - 1u))) atomicAdd(&s_hist[bin[k]], 1u);
+          if constexpr (!AT)
+            if (any[k] && lane == ((uint32_t)k & (lanes - 1u))) atomicAdd(&s_hist[bin[k]], 1u);
         }
         // the batch's gradients are contiguous per unit: one block store each
         if (lane == 0) {
@@ -333,6 +343,8 @@ __global__ __launch_bounds__(kGradThreads) void bwd_grad_kernel(const BwdPlan pl
         }
       }
     } else {
+      float gw[VEC];
+      if constexpr (AT) widen<EV, VEC>(gr, gw);
       for (int l = 0; l < pl.L; ++l) {
         const BwdLevel& lv = pl.lv[l];
 #pragma unroll 1
@@ -358,21 +370,54 @@ __global__ __launch_bounds__(kGradThreads) void bwd_grad_kernel(const BwdPlan pl
             if (p0 + k >= pl.P) continue;
             const int s = l * pl.P + p0 + k;
             float o[DIM + 1];
-            sample_grads<DIM, EV, VEC>(lv, sm[k], raw[k], gr, (float)attp[s], lg, o);
+            const float a = (float)attp[s];
+            sample_grads<DIM, EV, VEC>(lv, sm[k], raw[k], gr, a, lg, o);
             if (lane == ((uint32_t)k & (lanes - 1u))) {
               gap[s] = (TC)o[0];
 #pragma unroll
               for (int d = 0; d < DIM; ++d) glp[s * DIM + d] = (TC)o[1 + d];
-              if (any[k]) atomicAdd(&s_hist[bin[k]], 1u);
+              if constexpr (!AT)
+                if (any[k]) atomicAdd(&s_hist[bin[k]], 1u);
+            }
+            if constexpr (AT) {
+              if (act && any[k]) {
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                  if (!corner_valid<DIM>(c, sm[k])) continue;
+                  const float cw = corner_weight<DIM>(c, sm[k]) * a;
+                  // off is the corner row's byte offset in the value slice of this launch,
+                  // channels of this lane included; the sums share its element layout
+                  float* dst = bf.scratch + off[k][c] / (uint32_t)EV::kBytes;
+#pragma unroll
+                  for (int e = 0; e < VEC; ++e) atomicAdd(dst + e, cw * gw[e]);
+                }
+              }
             }
           }
         }
       }
     }
   }
-  __syncthreads();
-  for (int i = threadIdx.x; i < pl.bins; i += kGradThreads)
-    bf.counts[((size_t)g * pl.bins + i) * pl.wgpg + w] = s_hist[i];
+  if constexpr (!AT) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < pl.bins; i += kGradThreads)
+      bf.counts[((size_t)g * pl.bins + i) * pl.wgpg + w] = s_hist[i];
+  }
+}
+
+// Atomic plans: round the fp32 sums to the value dtype, VEC elements per thread and step
+// (n is a multiple of VEC: C is).
+template <typename EV, int VEC>
+__global__ __launch_bounds__(kBlock) void bwd_round_kernel(const float* __restrict__ src,
+                                                           typename EV::T* __restrict__ dst,
+                                                           uint32_t n) {
+  const uint32_t stride = gridDim.x * (uint32_t)kBlock * VEC;
+  for (uint32_t i = (blockIdx.x * (uint32_t)kBlock + threadIdx.x) * VEC; i < n; i += stride) {
+    float v[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) v[e] = src[i + e];
+    store_vec<EV, VEC>(dst + i, v);
+  }
 }
 
 // ------------------------------------------------------------------ 2: column scan
@@ -889,6 +934,19 @@ hipError_t run_bwd_t(const BwdPlan& pl, const BwdBuffers& bf, hipStream_t s) {
   const uint32_t nbin_wg = (uint32_t)pl.groups * (uint32_t)pl.wgpg;
   const size_t hist_bytes = (size_t)pl.bins * sizeof(uint32_t);
   if (nbin_wg == 0) return hipErrorInvalidValue;
+  if (pl.atomic) {
+    const uint32_t n = pl.value_bytes / (uint32_t)EV::kBytes;  // Bc * K * H * C
+    hipError_t e = launch_zero_bytes(bf.scratch, (size_t)n * sizeof(float), s);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 0, -1, true>), dim3(nbin_wg),
+                       dim3(kGradThreads), 0, s, pl, bf);
+    uint32_t blocks = (n / VEC + kBlock - 1) / kBlock;
+    blocks = blocks < 1 ? 1 : (blocks > 8192 ? 8192 : blocks);
+    if (n) hipLaunchKernelGGL((bwd_round_kernel<EV, VEC>), dim3(blocks), dim3(kBlock), 0, s,
+                              static_cast<const float*>(bf.scratch),
+                              static_cast<typename EV::T*>(bf.grad_value), n);
+    return hipGetLastError();
+  }
   // compile-time lane-group size for the common 16-byte lane loads of 4 or 8 lanes per unit
   if (pl.P == 4 && pl.coords_aligned && pl.lpu_log2 == 2)
     hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 4, 2>), dim3(nbin_wg), dim3(kGradThreads),
@@ -988,8 +1046,11 @@ BwdSizes bwd_sizes(const BwdPlan& pl, uint64_t samples, int dim) {
   z.bin_start = (uint64_t)pl.T + 1;
   z.chunk_off = (uint64_t)pl.T + 1;
   z.chunk_tile = pl.max_chunks;
-  z.record_words = (samples > 0 ? samples : 1) * (uint64_t)(dim + 2);
-  z.scratch_floats = (uint64_t)pl.max_chunks * pl.rcells * pl.C;
+  z.record_words = pl.atomic ? 0u : (samples > 0 ? samples : 1) * (uint64_t)(dim + 2);
+  // atomic plans: one fp32 sum per grad_value element of a launch (groups << hg_log2 =
+  // batches * H)
+  z.scratch_floats = pl.atomic ? ((uint64_t)pl.groups << pl.hg_log2) * (uint64_t)pl.K * pl.C
+                               : (uint64_t)pl.max_chunks * pl.rcells * pl.C;
   z.value_h_bytes = pl.head_major ? (uint64_t)pl.value_bytes : 0u;
   auto al = [](uint64_t b) { return (b + 255) & ~(uint64_t)255; };
   z.total_bytes = al(z.counts * 4) + al(z.bin_start * 4) + al(z.chunk_off * 4) +

@@ -139,6 +139,9 @@ struct BwdPlan {
   int32_t coords_aligned;      // loc and attn are 16-byte aligned: per-batch block loads allowed
   int32_t mul24;               // every row stride and corner index fits 24-bit multiplies
   int32_t head_major;          // the sample-gradient kernel reads BwdBuffers::value_h
+  int32_t atomic;              // levels exceed the LDS binning (more than kMaxBinsLds tiles per
+                               // head): grad_value is scattered with fp32 atomics into
+                               // BwdBuffers::scratch, then rounded into grad_value
   float lo_g, hi_g;
   uint32_t value_bytes;
   uint32_t lds_g_bytes;        // bytes of the staged fp32 grad_out rows of a sub-batch
@@ -161,7 +164,7 @@ struct BwdBuffers {
   uint32_t* chunk_off;   // T + 1: first chunk of each tile; [T] = number of chunks
   uint32_t* chunk_tile;  // max_chunks: tile of each chunk
   uint32_t* records;     // (DIM + 2) words per record: id | flags, u_x, u_y[, u_z], attn
-  float* scratch;        // max_chunks * rcells * C fp32 partials
+  float* scratch;        // max_chunks * rcells * C fp32 partials; atomic plans: (Bc, K, H, C) fp32 sums
 };
 
 struct BwdSizes {

@@ -278,6 +278,30 @@ class ParitySuite:
         _, gv, gl, ga = self.run_fwd_bwd(value, shapes, loc, attn, grad_out)
         self.check_grads(value, shapes, loc, attn, grad_out, gv, gl, ga)
 
+    @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+    def test_levels_beyond_binning_atomic_path(self, dtype) -> None:
+        """Levels with more than 8192 tiles per head (the backward's LDS binning limit; 2D
+        1032 x 1024 cells in 16 x 8 tiles, 3D 72 x 128 x 128 in 4 x 4 x 8) take the atomic
+        grad_value path: fp32 sums scattered with global atomics, then rounded once. The
+        second, 15-cell level makes most samples collide on a few keys."""
+        ss = [(1032, 1024), (3, 5)] if self.dim == 2 else [(72, 128, 128), (3, 5, 1)]
+        nb = 2 if self.dim == 2 else 1
+        value, shapes, loc, attn = self.inputs(batch_size=nb, num_queries=64, num_heads=1,
+                                               dim_per_head=32, num_points=4, spatial_shapes=ss,
+                                               dtype=dtype)
+        grad_out = torch.randn(nb, 64, 32, generator=torch.Generator().manual_seed(5)).to(dtype)
+        out, gv, gl, ga = self.run_fwd_bwd(value, shapes, loc, attn, grad_out)
+        assert gv.dtype == dtype and torch.isfinite(gv.float()).all()
+        if dtype == torch.float32:
+            assert max_rel(out, brute.fwd(value, shapes, loc, attn, coord_f32=True)) <= FWD_TOL_F32
+            self.check_grads(value, shapes, loc, attn, grad_out, gv, gl, ga)
+        else:
+            vf, lf, af, gf = value.float(), loc.float(), attn.float(), grad_out.float()
+            assert max_rel(out.float(), brute.fwd(vf, shapes, lf, af, coord_f32=True)) <= FWD_TOL_HALF
+            bv, bl, ba = brute.bwd(vf, shapes, lf, af, gf, coord_f32=True)
+            assert max_rel(gv.float(), bv) <= FWD_TOL_HALF
+            assert max_rel(ga.float(), ba) <= FWD_TOL_HALF
+
     def test_empty_inputs(self) -> None:
         value, shapes, loc, attn = self.inputs(batch_size=2, num_queries=0)
         out = self.fwd(*self.gpu(value), shapes, *self.gpu(loc, attn))

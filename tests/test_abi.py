@@ -116,16 +116,18 @@ def test_bwd_workspace_bytes_host_only():
     assert lib.msda_bwd_workspace_bytes(ctypes.byref(d3), _shapes(s3)) > 0
 
 
-def test_bwd_tile_limit_is_a_clear_error():
+def test_bwd_levels_beyond_binning_plan_atomic_path():
     """The backward bins samples by tile in LDS, at most 8192 tiles per head: a 2D bf16
-    C=32 level of 1024 x 1024 cells (64 x 128 tiles of 16 x 8) fits exactly; one more tile
-    row is refused with a message, before any device work."""
+    C=32 level of 1024 x 1024 cells (64 x 128 tiles of 16 x 8) is binned; one more tile row
+    switches the plan to the atomic grad_value path, whose workspace holds one fp32 sum per
+    grad_value element (host-only)."""
     lib = _lib.load()
     ok = _desc(batch=1, num_keys=1024 * 1024, num_queries=64, num_levels=1, num_heads=1)
-    assert lib.msda_bwd_workspace_bytes(ctypes.byref(ok), _shapes((1024, 1024))) > 0
-    big = _desc(batch=1, num_keys=1032 * 1024, num_queries=64, num_levels=1, num_heads=1)
-    assert lib.msda_bwd_workspace_bytes(ctypes.byref(big), _shapes((1032, 1024))) == 0
-    assert "levels too large (8256 tiles per head; the binning supports 8192)" in _lib.last_error()
+    binned = lib.msda_bwd_workspace_bytes(ctypes.byref(ok), _shapes((1024, 1024)))
+    assert binned > 0, _lib.last_error()
+    big = _desc(batch=2, num_keys=1032 * 1024, num_queries=64, num_levels=1, num_heads=2)
+    ws = lib.msda_bwd_workspace_bytes(ctypes.byref(big), _shapes((1032, 1024)))
+    assert ws >= 2 * 1032 * 1024 * 2 * 32 * 4, _lib.last_error()
 
 
 def test_fwd_workspace_bytes_rule():
