@@ -229,10 +229,8 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
                   lay.vec_bytes);
   const int s = elem_bytes(d->value_dtype);
   const int nc = 1 << d->dim;
-  if ((uint64_t)d->num_queries * d->num_points > (uint64_t)msda::kRecIdMask)
-    return fail(MSDA_ERR_INVALID,
-                "backward supports Q*P up to 2^27 per launch, got Q=%lld P=%d",
-                (long long)d->num_queries, d->num_points);
+  // records name their sample by q * P + p in 27 bits
+  const bool ids_fit = (uint64_t)d->num_queries * d->num_points <= (uint64_t)msda::kRecIdMask;
   // Tile extents and sub-batch size: start from 16x16 (2D) / 8x8x8 (3D) cells and
   // S = kTileThreads<dim> records (one per thread); halve the largest tile extent until a thread
   // owns at most kTileMaxItems (region cell, owner chunk) items, and lower S in steps of
@@ -309,15 +307,16 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
   pl.lds_g_bytes = S * grow;
   pl.lds_bytes = lds;
   // Levels with more than kMaxBinsLds tiles per head in total do not fit the LDS binning
-  // of the sample-gradient and fill kernels: such plans scatter grad_value with fp32
-  // atomics instead (sample-gradient kernel only, then one rounding pass).
+  // of the sample-gradient and fill kernels, and more than 2^27 samples per (b, h, level)
+  // do not fit a record id: such plans scatter grad_value with fp32 atomics instead
+  // (sample-gradient kernel only, then one rounding pass).
   int64_t all_tiles = 0;
   for (int l = 0; l < d->num_levels; ++l) {
     const msda::BwdLevel& lv = pl.lv[l];
     all_tiles += (int64_t)((lv.W + pl.TX - 1) / pl.TX) * ((lv.H + pl.TY - 1) / pl.TY) *
                  ((lv.D + pl.TZ - 1) / pl.TZ);
   }
-  const bool atomic = all_tiles > kMaxBinsLds;
+  const bool atomic = all_tiles > kMaxBinsLds || !ids_fit;
   pl.atomic = atomic ? 1 : 0;
   // tiles of the coarsest level first: its chunks are the longest, so they start early
   int tiles = 0;

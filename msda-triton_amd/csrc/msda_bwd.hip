@@ -37,8 +37,9 @@
 // Every grad_value element is written exactly once with a plain store, so no clearing
 // pass is needed and 16-bit values are rounded once, from fp32.
 //
-// Pyramids beyond the LDS binning (more than kMaxBinsLds tiles per head) run step 1 alone
-// with global fp32 atomics into fp32 sums in the workspace, then one rounding pass.
+// Pyramids beyond the LDS binning (more than kMaxBinsLds tiles per head) and launches whose
+// Q * P exceeds a record's 27-bit sample id run step 1 alone with global fp32 atomics into
+// fp32 sums in the workspace, then one rounding pass.
 #include "msda_internal.h"
 #include "msda_sample.h"
 

@@ -128,6 +128,16 @@ def test_bwd_levels_beyond_binning_plan_atomic_path():
     big = _desc(batch=2, num_keys=1032 * 1024, num_queries=64, num_levels=1, num_heads=2)
     ws = lib.msda_bwd_workspace_bytes(ctypes.byref(big), _shapes((1032, 1024)))
     assert ws >= 2 * 1032 * 1024 * 2 * 32 * 4, _lib.last_error()
+    # more than 2^27 samples per (b, h, level) do not fit a record's sample id: same plan,
+    # workspace = fp32 sums (plus 256-byte aligned bookkeeping), no records
+    q = (1 << 23) + 1
+    many = _desc(batch=1, num_keys=32 * 32, num_queries=q, num_levels=1, num_points=16,
+                 num_heads=1)
+    ws = lib.msda_bwd_workspace_bytes(ctypes.byref(many), _shapes((32, 32)))
+    assert 32 * 32 * 32 * 4 <= ws < q * 16 * 4, _lib.last_error()
+    fewer = _desc(batch=1, num_keys=32 * 32, num_queries=q - 2, num_levels=1, num_points=16,
+                  num_heads=1)  # 2^27 - 16 samples: binned, 16-byte records
+    assert lib.msda_bwd_workspace_bytes(ctypes.byref(fewer), _shapes((32, 32))) > q * 16 * 4
 
 
 def test_fwd_workspace_bytes_rule():
