@@ -172,15 +172,19 @@ def _op(dim, fwd_only=False):
     return msda_triton.msda3d_fused_fwd if fwd_only else msda_triton.msda3d_fused
 
 
-def _unfused(dim, value, shapes, ref, off, logits):
-    """The plain HIP op on the locations and weights formed in fp32 by torch on the GPU."""
+def _unfused(dim, value, shapes, ref, off, logits, autograd=False):
+    """The plain HIP op on the locations and weights formed in fp32 by torch on the GPU
+    (the autograd op with autograd=True, else the forward-only entry)."""
     B, Q, H, L, P, _ = off.shape
     inv = 1.0 / shapes.flip(-1).to(device=off.device, dtype=torch.float32)  # fp32 reciprocals
     # fma(off, inv, ref): the float64 product of two fp32 values is exact, one rounding after
     loc = (off.double() * inv.double()[None, None, None, :, None, :]
            + ref.double().expand(B, Q, L, dim)[:, :, None, :, None, :]).float()
     attn = logits.float().reshape(B, Q, H, L * P).softmax(-1).view(B, Q, H, L, P)
-    fn = msda_triton.msda2d_fwd if dim == 2 else msda_triton.msda3d_fwd
+    if autograd:
+        fn = msda_triton.msda2d if dim == 2 else msda_triton.msda3d
+    else:
+        fn = msda_triton.msda2d_fwd if dim == 2 else msda_triton.msda3d_fwd
     return fn(value, shapes, loc.contiguous(), attn.contiguous())
 
 
@@ -211,7 +215,41 @@ def test_backward_matches_oracle(dim, ref_levels):
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     print(f"fused bwd dim={dim} ref_levels={ref_levels}", flush=True)
-    value, shapes, ref, off, logits = _inputs(dim, torch.float32, ref_levels=ref_levels, Q=23)
+    _check_backward(dim, *_inputs(dim, torch.float32, ref_levels=ref_levels, Q=23))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dim", [2, 3])
+def test_backward_beyond_binning_matches_unfused(dim):
+    """A pyramid with more than 8192 backward tiles per head: the inner backward takes the
+    atomic grad_value plan (fp32 sums with global atomics, then one rounding pass). At 1024
+    cells per axis one fp32 ulp of a location moves the pixel coordinate by ~6e-5 px, so
+    the reference here is the plain autograd op on the same fp32 locations (formed with one
+    rounding, as the kernels form them) and torch's softmax; the plain op itself is checked
+    on such levels against the brute-force oracle with fp32 coordinates
+    (tests/_parity.py::test_levels_beyond_binning_atomic_path)."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    print(f"fused bwd beyond binning dim={dim}", flush=True)
+    shapes = [(1032, 1024), (3, 5)] if dim == 2 else [(72, 128, 128), (3, 5, 1)]
+    value, shapes, ref, off, logits = _inputs(dim, torch.float32, Q=23, B=1, H=1, shapes=shapes)
+    g = torch.Generator().manual_seed(11)
+    grad = torch.randn(1, 23, value.shape[2] * value.shape[3], generator=g).to(value.device)
+    a = [t.detach().clone().requires_grad_(True) for t in (value, ref, off, logits)]
+    out = _op(dim)(a[0], shapes, *a[1:])
+    out.backward(grad)
+    b = [t.detach().clone().requires_grad_(True) for t in (value, ref, off, logits)]
+    want = _unfused(dim, b[0], shapes, *b[1:], autograd=True)
+    want.backward(grad)
+    assert max_rel(out.detach(), want.detach()) <= 1e-6
+    for name, x, y in zip(("value", "ref", "off", "logits"), a, b):
+        assert x.grad is not None and x.grad.shape == y.grad.shape, name
+        err = max_rel(x.grad, y.grad)
+        assert err <= 1e-4, (name, err)
+
+
+def _check_backward(dim, value, shapes, ref, off, logits):
+    """Fused forward + backward on the GPU against the float64 oracle composition."""
     g = torch.Generator().manual_seed(11)
     grad = torch.randn(value.shape[0], off.shape[1], value.shape[2] * value.shape[3], generator=g)
     ins = [t.detach().clone().requires_grad_(True) for t in (value, ref, off, logits)]
