@@ -31,6 +31,9 @@ _LEVEL_CACHE_MAX = 64
 # that tensor is alive and unmodified (same version counter): a loop over one shapes
 # tensor pays the device-side conversion once.
 _GPU_LEVEL_CACHE: OrderedDict = OrderedDict()
+# The same identity cache for CPU-resident shape tensors (entries also hold K): a loop over
+# one shapes tensor skips reading it back into Python on every call.
+_CPU_ID_CACHE: OrderedDict = OrderedDict()
 
 
 def validate_inputs(name: str, dim: int, value: torch.Tensor, value_spatial_shapes: torch.Tensor,
@@ -120,37 +123,71 @@ def prepare_levels(dim: int, value: torch.Tensor, value_spatial_shapes: torch.Te
     """
     device = value.device
     if value_spatial_shapes.device.type == "cpu":
-        shapes_cpu = value_spatial_shapes.detach().to(dtype=torch.int64)
-        rows = tuple(tuple(int(v) for v in r) for r in shapes_cpu.tolist())
-        key = (dim, rows, device)
-        sizes = [1] * len(rows)
-        for i, r in enumerate(rows):
-            for v in r:
-                sizes[i] *= v
-        total_keys = sum(sizes)
-        if total_keys > _INT32_MAX:
-            raise ValueError(
-                f"Total number of keys ({total_keys}) exceeds int32 range. "
-                "Reduce spatial dimensions or number of levels."
-            )
-        if value.size(1) != total_keys:
-            raise ValueError(
-                f"value dim 1 ({value.size(1)}) does not match sum of spatial shapes "
-                f"({total_keys}). Ensure K = Σ({_SHAPE_NAMES[dim]}) across all levels."
-            )
-        hit = _LEVEL_CACHE.get(key)
+        key = id(value_spatial_shapes)
+        hit = _CPU_ID_CACHE.get(key)
         if hit is not None:
-            _LEVEL_CACHE.move_to_end(key)
-            return hit
-        starts = [0] * len(rows)
-        for i in range(1, len(rows)):
-            starts[i] = starts[i - 1] + sizes[i - 1]
-        host = torch.tensor(rows, dtype=torch.int32).reshape(len(rows), dim).contiguous()
-        levels = Levels(host.to(device), torch.tensor(starts, dtype=torch.int32).to(device), host)
-        _LEVEL_CACHE[key] = levels
-        if len(_LEVEL_CACHE) > _LEVEL_CACHE_MAX:
-            _LEVEL_CACHE.popitem(last=False)
+            ref, version, hdim, hdev, total_keys, levels = hit
+            if (ref() is value_spatial_shapes and version == value_spatial_shapes._version
+                    and hdim == dim and hdev == device):
+                _check_num_keys(dim, value, total_keys)
+                _CPU_ID_CACHE.move_to_end(key)
+                return levels
+            del _CPU_ID_CACHE[key]
+        levels, total_keys = _cpu_levels(dim, value, value_spatial_shapes)
+        try:
+            ref = weakref.ref(value_spatial_shapes)
+        except TypeError:
+            return levels
+        _CPU_ID_CACHE[key] = (ref, value_spatial_shapes._version, dim, device, total_keys, levels)
+        if len(_CPU_ID_CACHE) > _LEVEL_CACHE_MAX:
+            _CPU_ID_CACHE.popitem(last=False)
         return levels
+    return _gpu_levels(dim, value, value_spatial_shapes)
+
+
+def _check_num_keys(dim: int, value: torch.Tensor, total_keys: int) -> None:
+    if value.size(1) != total_keys:
+        raise ValueError(
+            f"value dim 1 ({value.size(1)}) does not match sum of spatial shapes "
+            f"({total_keys}). Ensure K = Σ({_SHAPE_NAMES[dim]}) across all levels."
+        )
+
+
+def _cpu_levels(dim: int, value: torch.Tensor, value_spatial_shapes: torch.Tensor):
+    """(levels, K) for CPU-resident shapes; device tables cached by the shapes' values."""
+    device = value.device
+    shapes_cpu = value_spatial_shapes.detach().to(dtype=torch.int64)
+    rows = tuple(tuple(int(v) for v in r) for r in shapes_cpu.tolist())
+    key = (dim, rows, device)
+    sizes = [1] * len(rows)
+    for i, r in enumerate(rows):
+        for v in r:
+            sizes[i] *= v
+    total_keys = sum(sizes)
+    if total_keys > _INT32_MAX:
+        raise ValueError(
+            f"Total number of keys ({total_keys}) exceeds int32 range. "
+            "Reduce spatial dimensions or number of levels."
+        )
+    _check_num_keys(dim, value, total_keys)
+    hit = _LEVEL_CACHE.get(key)
+    if hit is not None:
+        _LEVEL_CACHE.move_to_end(key)
+        return hit, total_keys
+    starts = [0] * len(rows)
+    for i in range(1, len(rows)):
+        starts[i] = starts[i - 1] + sizes[i - 1]
+    host = torch.tensor(rows, dtype=torch.int32).reshape(len(rows), dim).contiguous()
+    levels = Levels(host.to(device), torch.tensor(starts, dtype=torch.int32).to(device), host)
+    _LEVEL_CACHE[key] = levels
+    if len(_LEVEL_CACHE) > _LEVEL_CACHE_MAX:
+        _LEVEL_CACHE.popitem(last=False)
+    return levels, total_keys
+
+
+def _gpu_levels(dim: int, value: torch.Tensor, value_spatial_shapes: torch.Tensor) -> Levels:
+    """Level tables for GPU-resident shapes, cached for the live, unmodified tensor."""
+    device = value.device
     key = id(value_spatial_shapes)
     hit = _GPU_LEVEL_CACHE.get(key)
     if hit is not None:
@@ -219,7 +256,10 @@ def _on_device(device: torch.device):
 
 
 def _stream(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The current torch stream of device (a tensor's device: its index is set), as the
+    raw hipStream_t handle torch.cuda.current_stream(device).cuda_stream returns, without
+    building a Stream object per call."""
+    return torch._C._cuda_getCurrentRawStream(device.index)
 
 
 def forward(dim: int, value: torch.Tensor, levels: Levels, loc: torch.Tensor, attn: torch.Tensor,

@@ -238,6 +238,21 @@ class ParitySuite:
         assert max_rel(b, torch_ref.msda_ref(value, new, loc, attn)) <= FWD_TOL_F32
         assert not torch.equal(a, b)
 
+    def test_cpu_shapes_reused_and_modified_in_place(self) -> None:
+        """CPU shapes tensors are cached by identity and version counter: a reused tensor
+        hits the cache, an in-place change of its first level (same K) is seen, and the
+        K check still runs on a cache hit."""
+        value, shapes, loc, attn = self.inputs(batch_size=1, num_queries=16)
+        v, lo, a = self.gpu(value, loc, attn)
+        for _ in range(2):
+            out = self.fwd(v, shapes, lo, a).cpu()
+            assert max_rel(out, torch_ref.msda_ref(value, shapes, loc, attn)) <= FWD_TOL_F32
+        shapes[0] = torch.tensor([16, 64] if self.dim == 2 else [5, 4, 5])
+        out = self.fwd(v, shapes, lo, a).cpu()
+        assert max_rel(out, torch_ref.msda_ref(value, shapes, loc, attn)) <= FWD_TOL_F32
+        with pytest.raises(ValueError, match="does not match sum of spatial shapes"):
+            self.fwd(v[:, :-1], shapes, lo, a)
+
     def test_non_contiguous_inputs(self) -> None:
         value, shapes, loc, attn = self.inputs(batch_size=2, num_queries=30)
         ref = torch_ref.msda_ref(value, shapes, loc, attn)
