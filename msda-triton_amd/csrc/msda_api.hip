@@ -361,6 +361,12 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
   pl.hg_log2 = hg;
   pl.bins = tiles << hg;
   pl.upw = (msda::kGradThreads >> lay.lpu_log2) * msda::kGradRounds;
+  if (d->dim == 3) {
+    const uint64_t upw2 = 2u * (uint64_t)pl.upw;
+    const uint64_t wgs2 = (uint64_t)(((uint64_t)d->batch * d->num_heads) >> hg) *
+                          ((((uint64_t)d->num_queries << hg) + upw2 - 1) / upw2);
+    if (wgs2 >= (uint64_t)msda::kGradWgsPerCu * kCus) pl.upw = (int32_t)upw2;
+  }
   pl.wgpg = (int32_t)((((uint64_t)d->num_queries << hg) + pl.upw - 1) / pl.upw);
   pl.R = (kChunkRecords + pl.S - 1) / pl.S * pl.S;
   pl.lpu_log2 = lay.lpu_log2;

@@ -430,12 +430,22 @@ __global__ __launch_bounds__(kBlock) void bwd_colscan_kernel(const BwdPlan pl, c
   if (t >= pl.T) return;  // the whole wave exits
   uint32_t* c = bf.counts + (size_t)t * pl.wgpg;
   uint32_t run = 0;
-  for (int base = 0; base < pl.wgpg; base += kWave) {
-    const int i = base + (int)lane;
-    const uint32_t v = i < pl.wgpg ? c[i] : 0u;
-    const uint32_t inc = wave_incl_scan(v);
-    if (i < pl.wgpg) c[i] = run + inc - v;
-    run += __shfl(inc, kWave - 1, kWave);
+  // four 64-count blocks per step: their loads are issued before the first scan
+  constexpr int U = 4;
+  for (int base = 0; base < pl.wgpg; base += U * kWave) {
+    uint32_t v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = base + u * kWave + (int)lane;
+      v[u] = i < pl.wgpg ? c[i] : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = base + u * kWave + (int)lane;
+      const uint32_t inc = wave_incl_scan(v[u]);
+      if (i < pl.wgpg) c[i] = run + inc - v[u];
+      run += __shfl(inc, kWave - 1, kWave);
+    }
   }
   if (lane == 0) bf.bin_start[t] = run;
 }

@@ -22,7 +22,12 @@ constexpr int tile_owner_vec(int vec) { return vec < 4 ? vec : 4; }
 constexpr int kTileWavesPerSimd = 4;  // tile-kernel occupancy target (128 VGPRs)
 constexpr int kFillStage = 2048;      // records staged in LDS per fill round
 constexpr int kGradThreads = 256;     // threads of the backward sample-gradient kernel
-constexpr int kGradRounds = 4;        // unit groups each of its threads handles in turn
+// unit groups each thread of the sample-gradient and fill kernels handles in turn. 3D
+// launches that keep at least kGradWgsPerCu workgroups per CU at twice as many rounds use
+// 2 * kGradRounds (C5 sample gradients 476 -> 464 us, fill 113 -> 110 us); 2D keeps
+// kGradRounds (C2: 114 us against 127 us at 8 rounds)
+constexpr int kGradRounds = 4;
+constexpr int kGradWgsPerCu = 2;
 // threads of the staged forward kernel: 12 waves per CU leave each lane 168 VGPRs, so
 // neither variant spills (at 1024 threads, 128 VGPRs, the plain kernel spilled 20-64 bytes
 // per lane and the fused one 70-116, and both ran slower; 512 and 896 threads were slower)
@@ -128,7 +133,7 @@ struct BwdPlan {
   int32_t tiles_per_bh;
   int32_t hg_log2;
   int32_t groups;              // (batches in launch) * H / HG
-  int32_t upw;                 // units (b, q, h) per bin workgroup: kGradRounds * kGradThreads / lanes per unit
+  int32_t upw;                 // units (b, q, h) per bin workgroup: rounds * kGradThreads / lanes per unit
   int32_t wgpg;                // bin workgroups per group: ceil(Q * HG / upw)
   int32_t bins;                // tiles_per_bh * HG; bin = tile_in_bh * HG + head_in_group
   uint32_t T;                  // groups * bins: tiles of this launch
