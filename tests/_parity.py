@@ -21,7 +21,7 @@ import torch
 import msda_triton
 from msda_triton import triton as mt_triton
 from oracle import brute, torch_ref
-from tests._util import make_inputs, max_abs, max_rel
+from tests._util import clamp_active, make_inputs, max_abs, max_rel
 
 FWD_TOL_F32 = 1e-5
 FWD_TOL_HALF = 1e-2
@@ -74,6 +74,17 @@ class ParitySuite:
         assert max_rel(gl[keep], tl[keep]) <= GRAD_TOL_F32, (
             f"grad_loc vs torch {max_rel(gl[keep], tl[keep])} "
             f"({int((~keep).sum()) // self.dim} edge samples excluded)")
+
+    def check_half_grad_loc(self, value, shapes, loc, attn, grad_out, gl, clamp_eps=1e-4):
+        """16-bit grad_sampling_locations against the float64 brute-force oracle on the
+        upcast inputs with the kernels' fp32 coordinate rounding (same corners on every
+        sample), normwise <= 1e-2; exactly zero on axes where the grid clamp was active."""
+        vf, lf, af, gf = (t.float() for t in (value, loc, attn, grad_out))
+        _, bl, _ = brute.bwd(vf, shapes, lf, af, gf, True, clamp_eps, coord_f32=True)
+        gl = gl.float().cpu()
+        assert max_rel(gl, bl) <= FWD_TOL_HALF, f"grad_loc vs brute {max_rel(gl, bl)}"
+        active = torch.from_numpy(clamp_active(lf, clamp_eps))
+        assert torch.all(gl[active] == 0)
 
     # ------------------------------------------------------- reference-mirrored cases
     def test_forward_pass_basic(self) -> None:
@@ -200,6 +211,30 @@ class ParitySuite:
                                                  grad_out.to(dtype).float())
         assert max_rel(gv.float(), tv) <= FWD_TOL_HALF
         assert max_rel(ga.float(), ta) <= FWD_TOL_HALF
+        self.check_half_grad_loc(value, shapes, loc, attn, grad_out.to(dtype), gl)
+
+    @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+    def test_half_precision_clamped_points(self, dtype) -> None:
+        """16-bit locations on and beyond the level borders (0, 1, -0.1, 1.1 and within the
+        clamp band, about a fifth of all coordinates): grad_sampling_locations against the
+        float64 oracle, and exactly zero on every clamped axis."""
+        value, shapes, loc, attn = self.inputs(batch_size=2, num_queries=40, num_heads=4,
+                                               dim_per_head=32)
+        g = torch.Generator().manual_seed(9)
+        pick = torch.rand(loc.shape, generator=g) < 0.2
+        special = torch.tensor([0.0, 1.0, -0.1, 1.1, 2e-5, 1.0 - 2e-5, 3e-3])
+        idx = torch.randint(0, len(special), loc.shape, generator=g)
+        loc = torch.where(pick, special[idx], loc)
+        value, loc, attn = (t.to(dtype) for t in (value, loc, attn))
+        grad_out = torch.randn(2, 40, 4 * 32, generator=g).to(dtype)
+        out, gv, gl, ga = self.run_fwd_bwd(value, shapes, loc, attn, grad_out)
+        ref = brute.fwd(value.float(), shapes, loc.float(), attn.float(), coord_f32=True)
+        assert max_rel(out.float(), ref) <= FWD_TOL_HALF
+        assert int(torch.from_numpy(clamp_active(loc.float())).sum()) > 50
+        self.check_half_grad_loc(value, shapes, loc, attn, grad_out, gl)
+        bv, _, ba = brute.bwd(value.float(), shapes, loc.float(), attn.float(), grad_out.float(),
+                              coord_f32=True)
+        assert max_rel(gv.float(), bv) <= FWD_TOL_HALF and max_rel(ga.float(), ba) <= FWD_TOL_HALF
 
     # ------------------------------------------------------------- added cases
     def test_mixed_dtype_fp32_coords(self) -> None:
@@ -217,6 +252,10 @@ class ParitySuite:
                                                  grad_out.to(torch.bfloat16).float())
         assert max_rel(ga, ta) <= FWD_TOL_HALF
         assert max_rel(gv.float(), tv) <= FWD_TOL_HALF
+        # fp32 locations and weights: their gradients are computed and stored in fp32
+        bv, bl, ba = brute.bwd(vb.float(), shapes, loc, attn, grad_out.to(torch.bfloat16).float(),
+                               coord_f32=True)
+        assert max_rel(gl, bl) <= GRAD_TOL_F32 and max_rel(ga, ba) <= GRAD_TOL_F32
 
     def test_gpu_resident_shapes(self) -> None:
         value, shapes, loc, attn = self.inputs(batch_size=1)
@@ -316,6 +355,7 @@ class ParitySuite:
             bv, bl, ba = brute.bwd(vf, shapes, lf, af, gf, coord_f32=True)
             assert max_rel(gv.float(), bv) <= FWD_TOL_HALF
             assert max_rel(ga.float(), ba) <= FWD_TOL_HALF
+            assert max_rel(gl.float(), bl) <= FWD_TOL_HALF
 
     def test_empty_inputs(self) -> None:
         value, shapes, loc, attn = self.inputs(batch_size=2, num_queries=0)

@@ -42,3 +42,13 @@ def max_abs(a, b) -> float:
     a = torch.as_tensor(a).detach().double().cpu()
     b = torch.as_tensor(b).detach().double().cpu()
     return (a - b).abs().max().item()
+
+
+def clamp_active(loc, clamp_eps: float = 1e-4) -> np.ndarray:
+    """True per (sample, axis) where the grid clamp of the forward is active: the fp32 grid
+    coordinate g = 2*loc - 1 (rounded after each operation, as the kernels and torch's
+    fp32 oracle compute it) lies outside [fp32(-1 + eps), fp32(1 - eps)]. There the
+    gradient of the location is zero (backward of torch.clamp)."""
+    lo = np.asarray(torch.as_tensor(loc).detach().float().cpu().numpy(), dtype=np.float32)
+    g = np.float32(2.0) * lo - np.float32(1.0)
+    return (g < np.float32(-1.0 + clamp_eps)) | (g > np.float32(1.0 - clamp_eps))
