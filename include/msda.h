@@ -10,7 +10,8 @@
  *   value               (B, K, H, C)        value_dtype, contiguous
  *   spatial_shapes      (L, dim)  int32     rows are (H_l, W_l) for dim 2 and
  *                                           (D_l, H_l, W_l) for dim 3; device memory for
- *                                           msda_fwd, host memory for the backward calls
+ *                                           msda_fwd and msda_bwd_dev, host memory for
+ *                                           msda_bwd and msda_bwd_fused
  *   level_start         (L,)      int32     device memory (msda_fwd); exclusive prefix
  *                                           sum of the per-level sizes (row-major
  *                                           flattening of K)
@@ -34,7 +35,7 @@
 extern "C" {
 #endif
 
-#define MSDA_ABI_VERSION 3
+#define MSDA_ABI_VERSION 4
 
 typedef enum msda_dtype {
   MSDA_F32 = 0,
@@ -154,6 +155,43 @@ int msda_bwd(const msda_desc* desc,
              void* stream);
 
 /*
+ * Bytes of device workspace msda_bwd_dev needs for this descriptor (0 when there is nothing
+ * to sample), sized without the level shapes: from K it estimates the spatial tiles the
+ * backward bins samples into, and it adds an fp32 copy of grad_value for the atomic path the
+ * kernels fall back to on the device when the levels need more tiles than estimated (levels
+ * that are thin along an axis). Returns 0 and sets msda_last_error() if the descriptor is
+ * invalid.
+ */
+size_t msda_bwd_dev_workspace_bytes(const msda_desc* desc);
+
+/*
+ * msda_bwd with the level shapes in DEVICE memory (spatial_shapes as for msda_fwd). The
+ * host never reads them: the first kernel derives the tile geometry from them on the
+ * device, so the call neither copies the shapes to the host nor synchronises, and the
+ * whole sequence can be captured in a HIP graph. Results are those of msda_bwd on the same
+ * shapes, bit for bit in grad_sampling_locations and grad_attention_weights, and with the
+ * same fp32 accumulation of grad_value. If the shapes disagree with K (sum of the level
+ * sizes), every gradient is filled with NaN, since the error can no longer be returned.
+ * `workspace` must hold msda_bwd_dev_workspace_bytes() bytes, 256-byte aligned.
+ *
+ * Replaces the reference's backward for GPU-resident shapes, which reads the device level
+ * tables saved by the forward (src/msda_triton/triton/msda_2d.py:76-82, :799-851;
+ * src/msda_triton/triton/msda_3d.py:71-77, :942-996).
+ */
+int msda_bwd_dev(const msda_desc* desc,
+                 const int32_t* spatial_shapes,
+                 const void* value,
+                 const void* sampling_locations,
+                 const void* attention_weights,
+                 const void* grad_output,
+                 void* grad_value,
+                 void* grad_sampling_locations,
+                 void* grad_attention_weights,
+                 void* workspace,
+                 size_t workspace_bytes,
+                 void* stream);
+
+/*
  * Fused producer variant of msda_fwd: instead of sampling_locations and attention_weights
  * it reads what the attention modules produce before them, and forms both in fp32 inside
  * the kernel:
@@ -216,6 +254,36 @@ int msda_bwd_fused(const msda_desc* desc,
                    void* workspace,
                    size_t workspace_bytes,
                    void* stream);
+
+/* msda_bwd_fused_workspace_bytes for msda_bwd_fused_dev: sized without the level shapes, as
+ * msda_bwd_dev_workspace_bytes is. */
+size_t msda_bwd_fused_dev_workspace_bytes(const msda_desc* desc);
+
+/*
+ * msda_bwd_fused with the level shapes in DEVICE memory: the reciprocals of the level
+ * extents are computed on the device (the fused forward's division, so the locations are
+ * bit-identical) and the inner backward is msda_bwd_dev's. No host read of the shapes, no
+ * synchronisation. Same outputs as msda_bwd_fused on the same shapes.
+ *
+ * Replaces autograd through the reference modules' location and weight formation
+ * (src/msda_triton/pytorch/msda_2d.py:303-339, msda_3d.py:314-350) with GPU-resident
+ * shapes, followed by the GPU-shapes backward (src/msda_triton/triton/msda_2d.py:76-82,
+ * :799-851; msda_3d.py:71-77, :942-996).
+ */
+int msda_bwd_fused_dev(const msda_desc* desc,
+                       const int32_t* spatial_shapes,
+                       const void* value,
+                       const float* reference_points,
+                       const void* sampling_offsets,
+                       const void* attention_logits,
+                       const void* grad_output,
+                       void* grad_value,
+                       float* grad_reference_points,
+                       void* grad_sampling_offsets,
+                       void* grad_attention_logits,
+                       void* workspace,
+                       size_t workspace_bytes,
+                       void* stream);
 
 #ifdef __cplusplus
 }

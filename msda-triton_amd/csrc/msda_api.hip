@@ -1,7 +1,8 @@
 // msda_api.hip — extern "C" entry points declared in include/msda.h.
 //
 // Host-side work per call: validate the descriptor, pick the kernel instantiation, plan
-// the backward's tile geometry from the host copy of the level shapes, split the batch
+// the backward's tile geometry (from a host copy of the level shapes, or, for shapes that
+// live on the device, from bounds on the host and the shapes on the device), split the batch
 // into launches whose byte offsets fit the 32-bit buffer addressing the kernels use, and
 // enqueue everything on the caller's stream. No allocation, no synchronisation, no global
 // mutable state except the thread-local error text.
@@ -179,41 +180,42 @@ void fill_params(const msda_desc* d, const Layout& lay, int64_t nb, msda::Params
 }
 
 // ---------------------------------------------------------------------------------------
-// Backward plan from the host level shapes.
+// Backward plan. With host shapes every size is exact; without them (device-resident
+// shapes) the bin capacity is estimated from K and the launch falls back, on the device,
+// to the atomic grad_value path when the levels need more bins.
 struct BwdHostPlan {
   msda::BwdPlan pl;
   msda::BwdSizes sz;
+  msda::GeomArgs ga;  // make_geom inputs (groups of a full launch)
   Layout lay;
   int64_t nb;
 };
 
+// Upper estimate of a pyramid's tiles from K alone: 1.5x the tiles its cells fill, plus a
+// few partial tiles per level. Levels that are thin along one axis can need more; their
+// launches take the atomic path on the device.
+int64_t estimate_tiles(const msda_desc* d, int cells) {
+  const int64_t area = ((int64_t)d->num_keys + cells - 1) / cells;
+  return area + area / 2 + 4 * ((int64_t)1 << d->dim) * d->num_levels + 64;
+}
+
 int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int nptr,
              BwdHostPlan* out) {
-  if (d->num_levels > 0 && !hs) return fail(MSDA_ERR_INVALID, "host spatial shapes are NULL");
   memset(out, 0, sizeof(*out));
   msda::BwdPlan& pl = out->pl;
+  const bool dev = hs == nullptr;  // planned without the shapes
   int64_t total = 0;
-  for (int l = 0; l < d->num_levels; ++l) {
+  for (int l = 0; l < d->num_levels && !dev; ++l) {
     int64_t n = 1;
     for (int k = 0; k < d->dim; ++k) {
       const int32_t v = hs[l * d->dim + k];
       if (v < 0) return fail(MSDA_ERR_INVALID, "spatial shape of level %d is negative", l);
       n *= v;
     }
-    pl.lv[l].start = (int32_t)total;
-    if (d->dim == 2) {
-      pl.lv[l].D = 1;
-      pl.lv[l].H = hs[2 * l];
-      pl.lv[l].W = hs[2 * l + 1];
-    } else {
-      pl.lv[l].D = hs[3 * l];
-      pl.lv[l].H = hs[3 * l + 1];
-      pl.lv[l].W = hs[3 * l + 2];
-    }
     total += n;
     if (total > (int64_t)kLim31) return fail(MSDA_ERR_INVALID, "Total number of keys exceeds int32 range");
   }
-  if (total != d->num_keys)
+  if (!dev && total != d->num_keys)
     return fail(MSDA_ERR_INVALID,
                 "value dim 1 (%lld) does not match sum of spatial shapes (%lld)",
                 (long long)d->num_keys, (long long)total);
@@ -306,50 +308,31 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
   pl.S = S;
   pl.lds_g_bytes = S * grow;
   pl.lds_bytes = lds;
-  // Levels with more than kMaxBinsLds tiles per head in total do not fit the LDS binning
-  // of the sample-gradient and fill kernels, and more than 2^27 samples per (b, h, level)
-  // do not fit a record id: such plans scatter grad_value with fp32 atomics instead
-  // (sample-gradient kernel only, then one rounding pass).
-  int64_t all_tiles = 0;
-  for (int l = 0; l < d->num_levels; ++l) {
-    const msda::BwdLevel& lv = pl.lv[l];
-    all_tiles += (int64_t)((lv.W + pl.TX - 1) / pl.TX) * ((lv.H + pl.TY - 1) / pl.TY) *
-                 ((lv.D + pl.TZ - 1) / pl.TZ);
+  // Tiles per head over all levels: exact from host shapes, else an estimate from K.
+  // Levels with more than kMaxBinsLds tiles per head do not fit the LDS binning of the
+  // sample-gradient and fill kernels, and more than 2^27 samples per (b, h, level) do not fit
+  // a record id: such plans scatter grad_value with fp32 atomics instead (sample-gradient
+  // kernel only, then one rounding pass).
+  int64_t tiles = 0;
+  for (int l = 0; l < d->num_levels && !dev; ++l) {
+    const int32_t* r = hs + l * d->dim;
+    const int32_t W = r[d->dim - 1], H = r[d->dim - 2], D = d->dim == 3 ? r[0] : 1;
+    tiles += (int64_t)msda::tiles_along(W, pl.TX) * msda::tiles_along(H, pl.TY) *
+             msda::tiles_along(D, pl.TZ);
   }
-  const bool atomic = all_tiles > kMaxBinsLds || !ids_fit;
-  pl.atomic = atomic ? 1 : 0;
-  // tiles of the coarsest level first: its chunks are the longest, so they start early
-  int tiles = 0;
+  if (dev) tiles = estimate_tiles(d, pl.cells);
+  const bool atomic = (!dev && tiles > kMaxBinsLds) || !ids_fit;
+  pl.static_atomic = atomic ? 1 : 0;
+  pl.fallback = dev && !atomic ? 1 : 0;
+  if (atomic) tiles = 0;
   const bool head_major = !atomic && use_head_major(d);
-  bool mul24 = (uint64_t)(head_major ? 1 : d->num_heads) * d->channels * s < (1u << 23);
-  for (int l = d->num_levels - 1; l >= 0; --l) {
-    msda::BwdLevel& lv = pl.lv[l];
-    // bytes between rows of K (one head's rows are contiguous in the head-major copy)
-    const uint64_t rsb = (uint64_t)(head_major ? 1 : d->num_heads) * d->channels * s;
-    lv.base = (uint32_t)((uint64_t)lv.start * rsb);
-    lv.sy = (int32_t)((uint64_t)lv.W * rsb);
-    lv.sz = (int32_t)((uint64_t)lv.W * lv.H * rsb);
-    {
-      // largest stride used (y in 2D, z in 3D) and largest corner index must fit 24 bits
-      const uint64_t lim = 1u << 23;
-      const uint64_t top = (uint64_t)lv.W * (d->dim == 3 ? (uint64_t)lv.H : 1u) * rsb;
-      const int64_t ext = (lv.W > lv.H ? (lv.W > lv.D ? lv.W : lv.D) : (lv.H > lv.D ? lv.H : lv.D)) + 2;
-      if (top >= lim || (uint64_t)ext >= lim) mul24 = false;
-    }
-    lv.ntx = (lv.W + pl.TX - 1) / pl.TX;
-    lv.nty = (lv.H + pl.TY - 1) / pl.TY;
-    lv.ntz = (lv.D + pl.TZ - 1) / pl.TZ;
-    lv.tile_off = tiles;
-    const int64_t nt = atomic ? 0 : (int64_t)lv.ntx * lv.nty * lv.ntz;
-    lv.ntiles = (int32_t)nt;
-    tiles += (int)nt;
-  }
   // Heads whose rows share 128-byte lines are grouped (their units and chunks run on one
   // XCD). A head-major copy shares no lines across heads: one head per group then keeps
   // one head's value and grad_out rows per XCD (C5: tile 699 -> 523 us, sample gradients
   // 465 -> 449 us, fill 110 -> 105 us).
   int hg = head_major ? 0 : lay.hg_log2;
-  while (hg > 0 && ((int64_t)tiles << hg) > kMaxBinsLds) --hg;
+  while (hg > 0 && (tiles << hg) > kMaxBinsLds) --hg;
+  const int64_t bins_cap = (tiles << hg) < kMaxBinsLds ? (tiles << hg) : kMaxBinsLds;
   pl.L = d->num_levels;
   pl.P = d->num_points;
   pl.C = d->channels;
@@ -359,11 +342,9 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
   pl.div_p = msda::make_fastdiv((uint32_t)(d->num_points > 0 ? d->num_points : 1));
   pl.div_lp = msda::make_fastdiv((uint32_t)(d->num_levels * d->num_points > 0
                                                 ? d->num_levels * d->num_points : 1));
-  pl.tiles_per_bh = tiles;
-  pl.mul24 = mul24 ? 1 : 0;
   pl.head_major = head_major ? 1 : 0;
   pl.hg_log2 = hg;
-  pl.bins = tiles << hg;
+  pl.bins_cap = (int32_t)bins_cap;
   pl.upw = (msda::kGradThreads >> lay.lpu_log2) * msda::kGradRounds;
   if (d->dim == 3) {
     const uint64_t upw2 = 2u * (uint64_t)pl.upw;
@@ -380,19 +361,35 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
   pl.hi_g = (float)(1.0 - d->clamp_eps);
   int64_t nb = batches_per_launch(d, lay);
   // the per-(bin workgroup, tile) count matrix must stay below 2^31 entries too
-  const uint64_t per_b_counts = (uint64_t)d->num_heads * tiles * (uint64_t)pl.wgpg;
+  const uint64_t per_b_counts = (uint64_t)(d->num_heads >> hg) * bins_cap * (uint64_t)pl.wgpg;
   if (per_b_counts > kLim31) return fail(MSDA_ERR_INVALID, "backward count matrix too large");
   if (per_b_counts) nb = min64(nb, (int64_t)(kLim31 / per_b_counts));
   if (nb < 1) nb = 1;
   out->nb = nb;
   pl.groups = (int32_t)((nb * d->num_heads) >> hg);
-  pl.T = (uint32_t)pl.groups * (uint32_t)pl.bins;
+  pl.T_cap = (uint32_t)pl.groups * (uint32_t)bins_cap;
   const uint64_t samples =
       (uint64_t)nb * d->num_queries * d->num_heads * d->num_levels * d->num_points;
-  pl.max_chunks = atomic ? 0u : pl.T + (uint32_t)((samples + pl.R - 1) / pl.R);
+  pl.max_chunks = atomic ? 0u : pl.T_cap + (uint32_t)((samples + pl.R - 1) / pl.R);
   pl.grid_chunks = (pl.max_chunks + msda::kXcds - 1) / msda::kXcds * msda::kXcds;
   pl.value_bytes = (uint32_t)(nb * (uint64_t)d->num_keys * d->num_heads * d->channels * s);
+  pl.grad_loc_elems = samples * (uint64_t)d->dim;
   out->sz = msda::bwd_sizes(pl, samples, d->dim);
+  msda::GeomArgs& ga = out->ga;
+  ga.dim = d->dim;
+  ga.L = d->num_levels;
+  ga.H = d->num_heads;
+  ga.C = d->channels;
+  ga.s = s;
+  ga.head_major = pl.head_major;
+  ga.hg_log2 = hg;
+  ga.groups = pl.groups;
+  ga.TX = pl.TX;
+  ga.TY = pl.TY;
+  ga.TZ = pl.TZ;
+  ga.bins_cap = (int32_t)bins_cap;
+  ga.static_atomic = pl.static_atomic;
+  ga.K = d->num_keys;
   if (!msda::bwd_supported(d->dim, d->value_dtype, d->coord_dtype, lay.vec_bytes))
     return fail(MSDA_ERR_DTYPE, "no backward kernel for this dtype combination");
   return MSDA_OK;
@@ -401,6 +398,8 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
 void carve(char* ws, const msda::BwdSizes& z, msda::BwdBuffers* bf) {
   auto al = [](uint64_t b) { return (b + 255) & ~(uint64_t)255; };
   char* p = ws;
+  bf->geom = reinterpret_cast<const msda::BwdGeom*>(p);
+  p += al(z.geom_bytes);
   bf->counts = reinterpret_cast<uint32_t*>(p);
   p += al(z.counts * 4);
   bf->bin_start = reinterpret_cast<uint32_t*>(p);
@@ -413,6 +412,8 @@ void carve(char* ws, const msda::BwdSizes& z, msda::BwdBuffers* bf) {
   p += al(z.record_words * 4);
   bf->scratch = reinterpret_cast<float*>(p);
   p += al(z.scratch_floats * 4);
+  bf->sums = reinterpret_cast<float*>(p);
+  p += al(z.sum_floats * 4);
   bf->value_h = z.value_h_bytes ? p : nullptr;
 }
 
@@ -497,6 +498,7 @@ struct FusedWs {
   uint64_t total;
 };
 
+// hs == nullptr: the inner backward is planned without the shapes (msda_bwd_dev).
 bool fused_ws(const msda_desc* d, const int32_t* hs, FusedWs* w) {
   auto al = [](uint64_t b) { return (b + 255) & ~(uint64_t)255; };
   msda_desc d32 = *d;
@@ -515,14 +517,17 @@ bool fused_ws(const msda_desc* d, const int32_t* hs, FusedWs* w) {
   return true;
 }
 
-// Fused-path prep / grad launches over batch ranges that keep every index 32-bit.
-int run_fused_kernels(const msda_desc* d, const int32_t* hs, msda::FusedArgs a, bool grad,
-                      hipStream_t st) {
+// Fused-path prep / grad launches over batch ranges that keep every index 32-bit. The
+// reciprocals of the level extents come from the host shapes hs, or (hs == nullptr) are
+// computed by the kernels from the device shapes ds.
+int run_fused_kernels(const msda_desc* d, const int32_t* hs, const int32_t* ds,
+                      msda::FusedArgs a, bool grad, hipStream_t st) {
   Layout lay;
   const void* none[1] = {nullptr};
   int rc = choose_layout(d, none, 0, &lay);
   if (rc) return rc;
-  for (int l = 0; l < d->num_levels; ++l) {
+  a.shapes = hs ? nullptr : ds;
+  for (int l = 0; l < d->num_levels && hs; ++l) {
     const int32_t* r = hs + l * d->dim;
     // the forward kernel's reciprocals: 1.0f / (float)extent, correctly rounded on both sides
     a.inv[l][0] = 1.0f / (float)r[d->dim - 1];                   // W
@@ -566,6 +571,135 @@ int run_fused_kernels(const msda_desc* d, const int32_t* hs, msda::FusedArgs a, 
   }
   return MSDA_OK;
 }
+// Body of msda_bwd (hs: host shapes) and msda_bwd_dev (hs == nullptr, ds: device shapes).
+int bwd_impl(const msda_desc* d, const int32_t* hs, const int32_t* ds, const void* value,
+             const void* sampling_locations, const void* attention_weights,
+             const void* grad_output, void* grad_value, void* grad_sampling_locations,
+             void* grad_attention_weights, void* workspace, size_t workspace_bytes,
+             void* stream, const char* name) {
+  int rc = validate(d);
+  if (rc) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int sv = elem_bytes(d->value_dtype);
+  const size_t nval = (size_t)d->batch * (size_t)d->num_keys * d->num_heads * d->channels;
+  if (nval && !grad_value) return fail(MSDA_ERR_INVALID, "%s: grad_value is NULL", name);
+  const uint64_t units = (uint64_t)d->batch * d->num_queries * d->num_heads;
+  if (units == 0 || d->num_levels == 0 || d->num_points == 0) {
+    // no samples: grad_value is zero, the other gradients are empty
+    hipError_t e = msda::launch_zero_bytes(grad_value, nval * sv, st);
+    if (e != hipSuccess) return fail(MSDA_ERR_HIP, "%s clear failed: %s", name, hipGetErrorString(e));
+    return MSDA_OK;
+  }
+  if ((d->num_keys > 0 && !value) || !sampling_locations || !attention_weights || !grad_output ||
+      !grad_sampling_locations || !grad_attention_weights || (!hs && !ds))
+    return fail(MSDA_ERR_INVALID, "%s: required pointer is NULL", name);
+  const void* vptrs[3] = {value, grad_output, grad_value};
+  BwdHostPlan hp;
+  if ((rc = plan_bwd(d, hs, vptrs, 3, &hp))) return rc;
+  if (!workspace || workspace_bytes < hp.sz.total_bytes)
+    return fail(MSDA_ERR_WORKSPACE, "%s needs %llu workspace bytes, got %zu", name,
+                (unsigned long long)hp.sz.total_bytes, workspace_bytes);
+  if (((uintptr_t)workspace % 256) != 0)
+    return fail(MSDA_ERR_INVALID, "%s: workspace must be 256-byte aligned", name);
+
+  const int sc = elem_bytes(d->coord_dtype);
+  const uint64_t LP = (uint64_t)d->num_levels * d->num_points;
+  const uint64_t qh = (uint64_t)d->num_queries * d->num_heads;
+  const uint64_t kv = (uint64_t)d->num_keys * d->num_heads * d->channels;
+  msda::BwdBuffers bf{};
+  carve(static_cast<char*>(workspace), hp.sz, &bf);
+  msda::BwdGeom geom;
+  for (int64_t b0 = 0; b0 < d->batch; b0 += hp.nb) {
+    const int64_t bc = (d->batch - b0) < hp.nb ? (d->batch - b0) : hp.nb;
+    msda::BwdPlan pl = hp.pl;
+    msda::GeomArgs ga = hp.ga;
+    pl.groups = (int32_t)((bc * d->num_heads) >> pl.hg_log2);
+    pl.T_cap = (uint32_t)pl.groups * (uint32_t)pl.bins_cap;
+    pl.value_bytes = (uint32_t)(bc * kv * sv);
+    pl.grad_loc_elems = (uint64_t)bc * qh * LP * d->dim;
+    ga.groups = pl.groups;
+    if (hs) make_geom(ga, hs, &geom);
+    bf.value = static_cast<const char*>(value) + (uint64_t)b0 * kv * sv;
+    bf.loc = static_cast<const char*>(sampling_locations) + (uint64_t)b0 * qh * LP * d->dim * sc;
+    bf.attn = static_cast<const char*>(attention_weights) + (uint64_t)b0 * qh * LP * sc;
+    bf.grad_out = static_cast<const char*>(grad_output) + (uint64_t)b0 * qh * d->channels * sv;
+    bf.grad_value = static_cast<char*>(grad_value) + (uint64_t)b0 * kv * sv;
+    bf.grad_loc = static_cast<char*>(grad_sampling_locations) + (uint64_t)b0 * qh * LP * d->dim * sc;
+    bf.grad_attn = static_cast<char*>(grad_attention_weights) + (uint64_t)b0 * qh * LP * sc;
+    pl.coords_aligned = aligned(bf.loc, 16) && aligned(bf.attn, 16) && aligned(bf.grad_loc, 16) &&
+                        aligned(bf.grad_attn, 16);
+    if (pl.head_major) {
+      hipError_t e = msda::launch_head_major(bf.value, const_cast<void*>(bf.value_h), (uint32_t)bc,
+                                             (uint32_t)d->num_keys, (uint32_t)d->num_heads,
+                                             (uint32_t)(d->channels * sv), hp.lay.vec_bytes, st);
+      if (e != hipSuccess) return fail(MSDA_ERR_HIP, "%s relayout failed: %s", name, hipGetErrorString(e));
+    }
+    hipError_t e = msda::run_bwd(pl, hs ? &geom : nullptr, hs ? nullptr : &ga, ds, bf, d->dim,
+                                 d->value_dtype, d->coord_dtype, hp.lay.vec_bytes, st);
+    if (e != hipSuccess) return fail(MSDA_ERR_HIP, "%s launch failed: %s", name, hipGetErrorString(e));
+  }
+  return MSDA_OK;
+}
+
+// Body of msda_bwd_fused (hs: host shapes) and msda_bwd_fused_dev (hs == nullptr, ds:
+// device shapes).
+int fused_bwd_impl(const msda_desc* d, const int32_t* hs, const int32_t* ds, const void* value,
+                   const float* reference_points, const void* sampling_offsets,
+                   const void* attention_logits, const void* grad_output, void* grad_value,
+                   float* grad_reference_points, void* grad_sampling_offsets,
+                   void* grad_attention_logits, void* workspace, size_t workspace_bytes,
+                   void* stream, const char* name) {
+  int rc = validate(d);
+  if (rc) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const uint64_t units = (uint64_t)d->batch * d->num_queries * d->num_heads;
+  const uint64_t nref = (uint64_t)d->batch * d->num_queries * d->num_levels * d->dim;
+  if (units == 0 || d->num_levels == 0 || d->num_points == 0) {
+    // no samples: grad_value and grad_reference_points are zero, the others empty
+    const size_t nval = (size_t)d->batch * (size_t)d->num_keys * d->num_heads * d->channels;
+    if ((nval && !grad_value) || (nref && !grad_reference_points))
+      return fail(MSDA_ERR_INVALID, "%s: required pointer is NULL", name);
+    hipError_t e = msda::launch_zero_bytes(grad_value, nval * elem_bytes(d->value_dtype), st);
+    if (e == hipSuccess) e = msda::launch_zero_bytes(grad_reference_points, nref * 4, st);
+    if (e != hipSuccess) return fail(MSDA_ERR_HIP, "%s clear failed: %s", name, hipGetErrorString(e));
+    return MSDA_OK;
+  }
+  if (!reference_points || !sampling_offsets || !attention_logits || !grad_reference_points ||
+      !grad_sampling_offsets || !grad_attention_logits || (!hs && !ds))
+    return fail(MSDA_ERR_INVALID, "%s: required pointer is NULL", name);
+  FusedWs w;
+  if (!fused_ws(d, hs, &w)) return MSDA_ERR_INVALID;
+  if (!workspace || workspace_bytes < w.total)
+    return fail(MSDA_ERR_WORKSPACE, "%s needs %llu workspace bytes, got %zu", name,
+                (unsigned long long)w.total, workspace_bytes);
+  if (((uintptr_t)workspace % 256) != 0)
+    return fail(MSDA_ERR_INVALID, "%s: workspace must be 256-byte aligned", name);
+  char* ws = static_cast<char*>(workspace);
+  msda::FusedArgs a{};
+  a.ref = reference_points;
+  a.off = sampling_offsets;
+  a.logits = attention_logits;
+  a.loc = reinterpret_cast<float*>(ws + w.loc);
+  a.attn = reinterpret_cast<float*>(ws + w.attn);
+  // 1. the forward's fp32 locations and weights
+  if ((rc = run_fused_kernels(d, hs, ds, a, false, st))) return rc;
+  // 2. the ordinary backward on them
+  msda_desc d32 = *d;
+  d32.coord_dtype = MSDA_F32;
+  float* gloc = reinterpret_cast<float*>(ws + w.gloc);
+  float* gattn = reinterpret_cast<float*>(ws + w.gattn);
+  rc = bwd_impl(&d32, hs, ds, value, a.loc, a.attn, grad_output, grad_value, gloc, gattn,
+                ws + w.inner, w.inner_bytes, stream, name);
+  if (rc) return rc;
+  // 3. through the location and softmax formation
+  a.grad_loc = gloc;
+  a.grad_attn = gattn;
+  a.grad_ref = grad_reference_points;
+  a.grad_off = grad_sampling_offsets;
+  a.grad_logits = grad_attention_logits;
+  return run_fused_kernels(d, hs, ds, a, true, st);
+}
+
 }  // namespace
 
 extern "C" {
@@ -614,9 +748,21 @@ size_t msda_bwd_workspace_bytes(const msda_desc* d, const int32_t* host_spatial_
   if (validate(d)) return 0;
   const uint64_t units = (uint64_t)d->batch * d->num_queries * d->num_heads;
   if (units == 0 || d->num_levels == 0 || d->num_points == 0) return 0;
+  if (!host_spatial_shapes) return fail(MSDA_ERR_INVALID, "host spatial shapes are NULL"), 0;
   BwdHostPlan hp;
   const void* none[1] = {nullptr};
   if (plan_bwd(d, host_spatial_shapes, none, 0, &hp)) return 0;
+  return (size_t)hp.sz.total_bytes;
+}
+
+size_t msda_bwd_dev_workspace_bytes(const msda_desc* d) {
+  g_err[0] = 0;
+  if (validate(d)) return 0;
+  const uint64_t units = (uint64_t)d->batch * d->num_queries * d->num_heads;
+  if (units == 0 || d->num_levels == 0 || d->num_points == 0) return 0;
+  BwdHostPlan hp;
+  const void* none[1] = {nullptr};
+  if (plan_bwd(d, nullptr, none, 0, &hp)) return 0;
   return (size_t)hp.sz.total_bytes;
 }
 
@@ -626,63 +772,22 @@ int msda_bwd(const msda_desc* d, const int32_t* host_spatial_shapes, const void*
              void* grad_attention_weights, void* workspace, size_t workspace_bytes,
              void* stream) {
   g_err[0] = 0;
-  int rc = validate(d);
-  if (rc) return rc;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const int sv = elem_bytes(d->value_dtype);
-  const size_t nval = (size_t)d->batch * (size_t)d->num_keys * d->num_heads * d->channels;
-  if (nval && !grad_value) return fail(MSDA_ERR_INVALID, "msda_bwd: grad_value is NULL");
-  const uint64_t units = (uint64_t)d->batch * d->num_queries * d->num_heads;
-  if (units == 0 || d->num_levels == 0 || d->num_points == 0) {
-    // no samples: grad_value is zero, the other gradients are empty
-    hipError_t e = msda::launch_zero_bytes(grad_value, nval * sv, st);
-    if (e != hipSuccess) return fail(MSDA_ERR_HIP, "msda_bwd clear failed: %s", hipGetErrorString(e));
-    return MSDA_OK;
-  }
-  if ((d->num_keys > 0 && !value) || !sampling_locations || !attention_weights || !grad_output ||
-      !grad_sampling_locations || !grad_attention_weights)
-    return fail(MSDA_ERR_INVALID, "msda_bwd: required pointer is NULL");
-  const void* vptrs[3] = {value, grad_output, grad_value};
-  BwdHostPlan hp;
-  if ((rc = plan_bwd(d, host_spatial_shapes, vptrs, 3, &hp))) return rc;
-  if (!workspace || workspace_bytes < hp.sz.total_bytes)
-    return fail(MSDA_ERR_WORKSPACE, "msda_bwd needs %llu workspace bytes, got %zu",
-                (unsigned long long)hp.sz.total_bytes, workspace_bytes);
-  if (((uintptr_t)workspace % 256) != 0)
-    return fail(MSDA_ERR_INVALID, "msda_bwd: workspace must be 256-byte aligned");
+  if (d && d->num_levels > 0 && !host_spatial_shapes && validate(d) == MSDA_OK)
+    return fail(MSDA_ERR_INVALID, "host spatial shapes are NULL");
+  return bwd_impl(d, host_spatial_shapes, nullptr, value, sampling_locations, attention_weights,
+                  grad_output, grad_value, grad_sampling_locations, grad_attention_weights,
+                  workspace, workspace_bytes, stream, "msda_bwd");
+}
 
-  const int sc = elem_bytes(d->coord_dtype);
-  const uint64_t LP = (uint64_t)d->num_levels * d->num_points;
-  const uint64_t qh = (uint64_t)d->num_queries * d->num_heads;
-  const uint64_t kv = (uint64_t)d->num_keys * d->num_heads * d->channels;
-  msda::BwdBuffers bf{};
-  carve(static_cast<char*>(workspace), hp.sz, &bf);
-  for (int64_t b0 = 0; b0 < d->batch; b0 += hp.nb) {
-    const int64_t bc = (d->batch - b0) < hp.nb ? (d->batch - b0) : hp.nb;
-    msda::BwdPlan pl = hp.pl;
-    pl.groups = (int32_t)((bc * d->num_heads) >> pl.hg_log2);
-    pl.T = (uint32_t)pl.groups * (uint32_t)pl.bins;
-    pl.value_bytes = (uint32_t)(bc * kv * sv);
-    bf.value = static_cast<const char*>(value) + (uint64_t)b0 * kv * sv;
-    bf.loc = static_cast<const char*>(sampling_locations) + (uint64_t)b0 * qh * LP * d->dim * sc;
-    bf.attn = static_cast<const char*>(attention_weights) + (uint64_t)b0 * qh * LP * sc;
-    bf.grad_out = static_cast<const char*>(grad_output) + (uint64_t)b0 * qh * d->channels * sv;
-    bf.grad_value = static_cast<char*>(grad_value) + (uint64_t)b0 * kv * sv;
-    bf.grad_loc = static_cast<char*>(grad_sampling_locations) + (uint64_t)b0 * qh * LP * d->dim * sc;
-    bf.grad_attn = static_cast<char*>(grad_attention_weights) + (uint64_t)b0 * qh * LP * sc;
-    pl.coords_aligned = aligned(bf.loc, 16) && aligned(bf.attn, 16) && aligned(bf.grad_loc, 16) &&
-                        aligned(bf.grad_attn, 16);
-    if (pl.head_major) {
-      hipError_t e = msda::launch_head_major(bf.value, const_cast<void*>(bf.value_h), (uint32_t)bc,
-                                             (uint32_t)d->num_keys, (uint32_t)d->num_heads,
-                                             (uint32_t)(d->channels * sv), hp.lay.vec_bytes, st);
-      if (e != hipSuccess) return fail(MSDA_ERR_HIP, "msda_bwd relayout failed: %s", hipGetErrorString(e));
-    }
-    hipError_t e = msda::run_bwd(pl, bf, d->dim, d->value_dtype, d->coord_dtype,
-                                 hp.lay.vec_bytes, st);
-    if (e != hipSuccess) return fail(MSDA_ERR_HIP, "msda_bwd launch failed: %s", hipGetErrorString(e));
-  }
-  return MSDA_OK;
+int msda_bwd_dev(const msda_desc* d, const int32_t* spatial_shapes, const void* value,
+                 const void* sampling_locations, const void* attention_weights,
+                 const void* grad_output, void* grad_value, void* grad_sampling_locations,
+                 void* grad_attention_weights, void* workspace, size_t workspace_bytes,
+                 void* stream) {
+  g_err[0] = 0;
+  return bwd_impl(d, nullptr, spatial_shapes, value, sampling_locations, attention_weights,
+                  grad_output, grad_value, grad_sampling_locations, grad_attention_weights,
+                  workspace, workspace_bytes, stream, "msda_bwd_dev");
 }
 
 size_t msda_bwd_fused_workspace_bytes(const msda_desc* d, const int32_t* host_spatial_shapes) {
@@ -690,8 +795,19 @@ size_t msda_bwd_fused_workspace_bytes(const msda_desc* d, const int32_t* host_sp
   if (validate(d)) return 0;
   const uint64_t units = (uint64_t)d->batch * d->num_queries * d->num_heads;
   if (units == 0 || d->num_levels == 0 || d->num_points == 0) return 0;
+  if (!host_spatial_shapes) return fail(MSDA_ERR_INVALID, "host spatial shapes are NULL"), 0;
   FusedWs w;
   if (!fused_ws(d, host_spatial_shapes, &w)) return 0;
+  return (size_t)w.total;
+}
+
+size_t msda_bwd_fused_dev_workspace_bytes(const msda_desc* d) {
+  g_err[0] = 0;
+  if (validate(d)) return 0;
+  const uint64_t units = (uint64_t)d->batch * d->num_queries * d->num_heads;
+  if (units == 0 || d->num_levels == 0 || d->num_points == 0) return 0;
+  FusedWs w;
+  if (!fused_ws(d, nullptr, &w)) return 0;
   return (size_t)w.total;
 }
 
@@ -702,55 +818,25 @@ int msda_bwd_fused(const msda_desc* d, const int32_t* host_spatial_shapes, const
                    void* grad_attention_logits, void* workspace, size_t workspace_bytes,
                    void* stream) {
   g_err[0] = 0;
-  int rc = validate(d);
-  if (rc) return rc;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const uint64_t units = (uint64_t)d->batch * d->num_queries * d->num_heads;
-  const uint64_t nref = (uint64_t)d->batch * d->num_queries * d->num_levels * d->dim;
-  if (units == 0 || d->num_levels == 0 || d->num_points == 0) {
-    // no samples: grad_value and grad_reference_points are zero, the others empty
-    const size_t nval = (size_t)d->batch * (size_t)d->num_keys * d->num_heads * d->channels;
-    if ((nval && !grad_value) || (nref && !grad_reference_points))
-      return fail(MSDA_ERR_INVALID, "msda_bwd_fused: required pointer is NULL");
-    hipError_t e = msda::launch_zero_bytes(grad_value, nval * elem_bytes(d->value_dtype), st);
-    if (e == hipSuccess) e = msda::launch_zero_bytes(grad_reference_points, nref * 4, st);
-    if (e != hipSuccess) return fail(MSDA_ERR_HIP, "msda_bwd_fused clear failed: %s", hipGetErrorString(e));
-    return MSDA_OK;
-  }
-  if (!reference_points || !sampling_offsets || !attention_logits || !grad_reference_points ||
-      !grad_sampling_offsets || !grad_attention_logits)
-    return fail(MSDA_ERR_INVALID, "msda_bwd_fused: required pointer is NULL");
-  FusedWs w;
-  if (!fused_ws(d, host_spatial_shapes, &w)) return MSDA_ERR_INVALID;
-  if (!workspace || workspace_bytes < w.total)
-    return fail(MSDA_ERR_WORKSPACE, "msda_bwd_fused needs %llu workspace bytes, got %zu",
-                (unsigned long long)w.total, workspace_bytes);
-  if (((uintptr_t)workspace % 256) != 0)
-    return fail(MSDA_ERR_INVALID, "msda_bwd_fused: workspace must be 256-byte aligned");
-  char* ws = static_cast<char*>(workspace);
-  msda::FusedArgs a{};
-  a.ref = reference_points;
-  a.off = sampling_offsets;
-  a.logits = attention_logits;
-  a.loc = reinterpret_cast<float*>(ws + w.loc);
-  a.attn = reinterpret_cast<float*>(ws + w.attn);
-  // 1. the forward's fp32 locations and weights
-  if ((rc = run_fused_kernels(d, host_spatial_shapes, a, false, st))) return rc;
-  // 2. the ordinary backward on them
-  msda_desc d32 = *d;
-  d32.coord_dtype = MSDA_F32;
-  float* gloc = reinterpret_cast<float*>(ws + w.gloc);
-  float* gattn = reinterpret_cast<float*>(ws + w.gattn);
-  rc = msda_bwd(&d32, host_spatial_shapes, value, a.loc, a.attn, grad_output, grad_value, gloc,
-                gattn, ws + w.inner, w.inner_bytes, stream);
-  if (rc) return rc;
-  // 3. through the location and softmax formation
-  a.grad_loc = gloc;
-  a.grad_attn = gattn;
-  a.grad_ref = grad_reference_points;
-  a.grad_off = grad_sampling_offsets;
-  a.grad_logits = grad_attention_logits;
-  return run_fused_kernels(d, host_spatial_shapes, a, true, st);
+  if (d && d->num_levels > 0 && !host_spatial_shapes && validate(d) == MSDA_OK)
+    return fail(MSDA_ERR_INVALID, "host spatial shapes are NULL");
+  return fused_bwd_impl(d, host_spatial_shapes, nullptr, value, reference_points,
+                        sampling_offsets, attention_logits, grad_output, grad_value,
+                        grad_reference_points, grad_sampling_offsets, grad_attention_logits,
+                        workspace, workspace_bytes, stream, "msda_bwd_fused");
+}
+
+int msda_bwd_fused_dev(const msda_desc* d, const int32_t* spatial_shapes, const void* value,
+                       const float* reference_points, const void* sampling_offsets,
+                       const void* attention_logits, const void* grad_output, void* grad_value,
+                       float* grad_reference_points, void* grad_sampling_offsets,
+                       void* grad_attention_logits, void* workspace, size_t workspace_bytes,
+                       void* stream) {
+  g_err[0] = 0;
+  return fused_bwd_impl(d, nullptr, spatial_shapes, value, reference_points, sampling_offsets,
+                        attention_logits, grad_output, grad_value, grad_reference_points,
+                        grad_sampling_offsets, grad_attention_logits, workspace,
+                        workspace_bytes, stream, "msda_bwd_fused_dev");
 }
 
 }  // extern "C"

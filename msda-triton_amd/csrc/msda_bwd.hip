@@ -49,6 +49,18 @@ namespace {
 
 constexpr int kPlanThreads = 1024;
 
+// The launch's level geometry, read through the constant address space: the kernels never
+// write it, so wave-uniform fields become scalar loads.
+typedef const __attribute__((address_space(4))) BwdGeom* GeoP;
+
+__device__ inline GeoP geo_of(const BwdBuffers& bf) { return (GeoP)bf.geom; }
+
+__device__ inline BwdLevel level_at(GeoP g, int l) {
+  BwdLevel lv;
+  __builtin_memcpy(&lv, &g->lv[l], sizeof(BwdLevel));
+  return lv;
+}
+
 // ------------------------------------------------------------------ block scans
 __device__ inline uint32_t wave_incl_scan(uint32_t v) {
   const int lane = threadIdx.x & (kWave - 1);
@@ -86,23 +98,25 @@ struct TileCoord {
   int l, tx, ty, tz, X0, Y0, Z0;
 };
 
-__device__ inline int level_of_tile(const BwdPlan& pl, int tib) {
+__device__ inline int level_of_tile(const BwdPlan& pl, GeoP geo, int tib) {
   int l = 0;
-  while (l + 1 < pl.L && !(tib >= pl.lv[l].tile_off && tib < pl.lv[l].tile_off + pl.lv[l].ntiles)) ++l;
+  while (l + 1 < pl.L && !(tib >= geo->lv[l].tile_off && tib < geo->lv[l].tile_off + geo->lv[l].ntiles)) ++l;
   return l;
 }
 
-__device__ inline TileCoord decode_tile(const BwdPlan& pl, uint32_t t) {
+__device__ inline TileCoord decode_tile(const BwdPlan& pl, GeoP geo, uint32_t t, BwdLevel* lvp) {
   TileCoord tc;
-  tc.g = t / (uint32_t)pl.bins;
-  const uint32_t bin = t - tc.g * (uint32_t)pl.bins;
+  const uint32_t bins = (uint32_t)geo->bins;
+  tc.g = t / bins;
+  const uint32_t bin = t - tc.g * bins;
   tc.hsub = bin & ((1u << pl.hg_log2) - 1u);
   const int tib = (int)(bin >> pl.hg_log2);
   const uint32_t gph = (uint32_t)pl.H >> pl.hg_log2;
   tc.b = tc.g / gph;
   tc.h = ((tc.g - tc.b * gph) << pl.hg_log2) | tc.hsub;
-  tc.l = level_of_tile(pl, tib);
-  const BwdLevel& lv = pl.lv[tc.l];
+  tc.l = level_of_tile(pl, geo, tib);
+  const BwdLevel lv = level_at(geo, tc.l);
+  *lvp = lv;
   const int lt = tib - lv.tile_off;
   tc.tx = lt % lv.ntx;
   tc.ty = (lt / lv.ntx) % lv.nty;
@@ -201,9 +215,9 @@ __device__ inline void sample_grads(const BwdLevel& lv, const Sample<DIM>& sm,
 
 // Axes, corner-row offsets and anchor bin of one sample from its DIM coordinates.
 template <int DIM>
-__device__ inline bool sample_rows(const BwdPlan& pl, const BwdLevel& lv, const float* xyz,
-                                   uint32_t vbase, uint32_t rs, uint32_t hsub, Sample<DIM>& sm,
-                                   uint32_t (&off)[1 << DIM], uint32_t* bin) {
+__device__ inline bool sample_rows(const BwdPlan& pl, const BwdLevel& lv, bool mul24,
+                                   const float* xyz, uint32_t vbase, uint32_t rs, uint32_t hsub,
+                                   Sample<DIM>& sm, uint32_t (&off)[1 << DIM], uint32_t* bin) {
   bool px, py, pz = true;
   const float ux = grid_to_u(xyz[0], (float)lv.W, pl.clamp, pl.lo_g, pl.hi_g, &px);
   const float uy = grid_to_u(xyz[1], (float)lv.H, pl.clamp, pl.lo_g, pl.hi_g, &py);
@@ -219,7 +233,7 @@ __device__ inline bool sample_rows(const BwdPlan& pl, const BwdLevel& lv, const 
   }
   // byte offset of the lowest corner; 24-bit multiplies when the plan allows them
   int32_t o0;
-  if (pl.mul24) {
+  if (mul24) {
     o0 = __mul24(sm.ay.i0, lv.sy) + __mul24(sm.ax.i0, (int32_t)rs);
     if constexpr (DIM == 3) o0 += __mul24(sm.az.i0, lv.sz);
   } else {
@@ -251,8 +265,12 @@ __device__ inline bool sample_rows(const BwdPlan& pl, const BwdLevel& lv, const 
 // AT (plans whose levels exceed the LDS binning; PT == 0 only): instead of counting its
 // samples per tile, each lane adds attn * w_c * grad_out of its channels to every valid
 // corner row of the fp32 (Bc, K, H, C) sums in bf.scratch with global fp32 atomics.
+// The geometry: with host shapes (pl.geom_arg) the kernel argument hg, which workgroup 0
+// also stores in the workspace for the kernels after this one; else the workspace copy
+// bwd_geom_kernel wrote.
 template <int DIM, typename EV, typename EC, int VEC, int PT, int LG, bool AT = false>
-__global__ __launch_bounds__(kGradThreads) void bwd_grad_kernel(const BwdPlan pl, const BwdBuffers bf) {
+__global__ __launch_bounds__(kGradThreads) void bwd_grad_kernel(const BwdPlan pl, const BwdBuffers bf,
+                                                                const BwdGeom hg) {
   static_assert(!AT || PT == 0, "the atomic scatter is built on the generic sample loop");
   constexpr int VB = VEC * EV::kBytes;
   constexpr int NC = 1 << DIM;
@@ -260,12 +278,22 @@ __global__ __launch_bounds__(kGradThreads) void bwd_grad_kernel(const BwdPlan pl
   typedef typename EC::T TC;
   typedef typename EV::T TV;
   extern __shared__ uint32_t s_hist[];  // [bins]
+  const GeoP geo = pl.geom_arg ? (GeoP)&hg : geo_of(bf);
+  if (pl.geom_arg && blockIdx.x == 0) {
+    BwdGeom* dst = const_cast<BwdGeom*>(bf.geom);
+    for (uint32_t i = threadIdx.x; i < sizeof(BwdGeom) / 4; i += kGradThreads)
+      reinterpret_cast<uint32_t*>(dst)[i] = reinterpret_cast<const uint32_t*>(&hg)[i];
+  }
+  // launches planned without the shapes run both variants; the geometry selects one
+  if (AT ? (!geo->atomic || geo->invalid) : geo->atomic) return;
+  const int bins = geo->bins;
+  const bool mul24 = geo->mul24 != 0;
   // workgroups of one (batch, head-group) are contiguous and dealt to one XCD
   const uint32_t lb = xcd_logical_block(blockIdx.x, gridDim.x);
   const uint32_t g = lb / (uint32_t)pl.wgpg;
   const uint32_t w = lb - g * (uint32_t)pl.wgpg;
   if constexpr (!AT) {
-    for (int i = threadIdx.x; i < pl.bins; i += kGradThreads) s_hist[i] = 0;
+    for (int i = threadIdx.x; i < bins; i += kGradThreads) s_hist[i] = 0;
     __syncthreads();
   }
 
@@ -303,7 +331,7 @@ __global__ __launch_bounds__(kGradThreads) void bwd_grad_kernel(const BwdPlan pl
       }
 #pragma unroll 1
       for (int bi = 0; bi < nbatch; ++bi) {
-        const BwdLevel& lv = pl.lv[bi / BPL];
+        const BwdLevel lv = level_at(geo, bi / BPL);
         Sample<DIM> sm[SB];
         uint32_t off[SB][NC], bin[SB];
         bool any[SB];
@@ -314,7 +342,7 @@ __global__ __launch_bounds__(kGradThreads) void bwd_grad_kernel(const BwdPlan pl
 #pragma unroll
           for (int d = 0; d < DIM; ++d) xyz[d] = block_elem(cb, k * DIM + d);
           bin[k] = 0;
-          any[k] = sample_rows<DIM>(pl, lv, xyz, vbase, rs, bu.hsub, sm[k], off[k], &bin[k]);
+          any[k] = sample_rows<DIM>(pl, lv, mul24, xyz, vbase, rs, bu.hsub, sm[k], off[k], &bin[k]);
           a[k] = block_elem(ab, k);
         }
         RawVec<VB> raw[SB][NC];
@@ -347,7 +375,7 @@ __global__ __launch_bounds__(kGradThreads) void bwd_grad_kernel(const BwdPlan pl
       float gw[VEC];
       if constexpr (AT) widen<EV, VEC>(gr, gw);
       for (int l = 0; l < pl.L; ++l) {
-        const BwdLevel& lv = pl.lv[l];
+        const BwdLevel lv = level_at(geo, l);
 #pragma unroll 1
         for (int p0 = 0; p0 < pl.P; p0 += SB) {
           Sample<DIM> sm[SB];
@@ -362,7 +390,7 @@ __global__ __launch_bounds__(kGradThreads) void bwd_grad_kernel(const BwdPlan pl
 #pragma unroll
             for (int d = 0; d < DIM; ++d) xyz[d] = (float)locp[s * DIM + d];
             bin[k] = 0;
-            any[k] = sample_rows<DIM>(pl, lv, xyz, vbase, rs, bu.hsub, sm[k], off[k], &bin[k]);
+            any[k] = sample_rows<DIM>(pl, lv, mul24, xyz, vbase, rs, bu.hsub, sm[k], off[k], &bin[k]);
 #pragma unroll
             for (int c = 0; c < NC; ++c) raw[k][c] = buf_load<VB>(rv, live ? off[k][c] : kOobOffset);
           }
@@ -388,7 +416,7 @@ __global__ __launch_bounds__(kGradThreads) void bwd_grad_kernel(const BwdPlan pl
                   const float cw = corner_weight<DIM>(c, sm[k]) * a;
                   // off is the corner row's byte offset in the value slice of this launch,
                   // channels of this lane included; the sums share its element layout
-                  float* dst = bf.scratch + off[k][c] / (uint32_t)EV::kBytes;
+                  float* dst = bf.sums + off[k][c] / (uint32_t)EV::kBytes;
 #pragma unroll
                   for (int e = 0; e < VEC; ++e) atomicAdd(dst + e, cw * gw[e]);
                 }
@@ -401,23 +429,54 @@ __global__ __launch_bounds__(kGradThreads) void bwd_grad_kernel(const BwdPlan pl
   }
   if constexpr (!AT) {
     __syncthreads();
-    for (int i = threadIdx.x; i < pl.bins; i += kGradThreads)
-      bf.counts[((size_t)g * pl.bins + i) * pl.wgpg + w] = s_hist[i];
+    for (int i = threadIdx.x; i < bins; i += kGradThreads)
+      bf.counts[((size_t)g * bins + i) * pl.wgpg + w] = s_hist[i];
   }
 }
 
-// Atomic plans: round the fp32 sums to the value dtype, VEC elements per thread and step
-// (n is a multiple of VEC: C is).
-template <typename EV, int VEC>
-__global__ __launch_bounds__(kBlock) void bwd_round_kernel(const float* __restrict__ src,
-                                                           typename EV::T* __restrict__ dst,
-                                                           uint32_t n) {
+// Atomic path: clear the n fp32 sums (16-byte aligned) before the scatter.
+__global__ __launch_bounds__(kBlock) void bwd_clear_sums_kernel(const BwdPlan pl, const BwdBuffers bf,
+                                                                uint32_t n) {
+  if (!pl.static_atomic) {  // the geometry exists already only on the device-shapes path
+    const GeoP geo = geo_of(bf);
+    if (!geo->atomic || geo->invalid) return;
+  }
+  const uint32_t stride = gridDim.x * (uint32_t)kBlock * 4u;
+  for (uint32_t i = (blockIdx.x * (uint32_t)kBlock + threadIdx.x) * 4u; i < n; i += stride) {
+    if (i + 4u <= n) {
+      *reinterpret_cast<float4*>(bf.sums + i) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    } else {
+      for (uint32_t k = i; k < n; ++k) bf.sums[k] = 0.0f;
+    }
+  }
+}
+
+// Atomic path: round the fp32 sums to the value dtype, VEC elements per thread and step
+// (n is a multiple of VEC: C is). Invalid device shapes: every gradient becomes NaN
+// (n_loc grad_loc elements and n_attn = n_loc / DIM grad_attn elements in the coord dtype).
+template <typename EV, typename EC, int VEC>
+__global__ __launch_bounds__(kBlock) void bwd_round_kernel(const BwdBuffers bf, uint32_t n,
+                                                           uint64_t n_loc, int dim) {
+  const GeoP geo = geo_of(bf);
+  if (!geo->atomic) return;
+  const bool nan = geo->invalid != 0;
   const uint32_t stride = gridDim.x * (uint32_t)kBlock * VEC;
+  typename EV::T* dst = static_cast<typename EV::T*>(bf.grad_value);
   for (uint32_t i = (blockIdx.x * (uint32_t)kBlock + threadIdx.x) * VEC; i < n; i += stride) {
     float v[VEC];
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) v[e] = src[i + e];
+    for (int e = 0; e < VEC; ++e) v[e] = nan ? __builtin_nanf("") : bf.sums[i + e];
     store_vec<EV, VEC>(dst + i, v);
+  }
+  if (nan) {
+    typename EC::T* gl = static_cast<typename EC::T*>(bf.grad_loc);
+    typename EC::T* ga = static_cast<typename EC::T*>(bf.grad_attn);
+    const uint64_t st = (uint64_t)gridDim.x * kBlock;
+    const uint64_t n_attn = n_loc / (uint64_t)dim;
+    for (uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x; i < n_loc; i += st) {
+      gl[i] = narrow<EC>(__builtin_nanf(""));
+      if (i < n_attn) ga[i] = narrow<EC>(__builtin_nanf(""));
+    }
   }
 }
 
@@ -425,9 +484,10 @@ __global__ __launch_bounds__(kBlock) void bwd_round_kernel(const float* __restri
 // One wave per tile: the tile's counts over the bin workgroups of its group become
 // offsets within the tile, and its total goes to bin_start[t].
 __global__ __launch_bounds__(kBlock) void bwd_colscan_kernel(const BwdPlan pl, const BwdBuffers bf) {
+  const GeoP geo = geo_of(bf);
   const uint32_t t = blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
   const uint32_t lane = threadIdx.x & (kWave - 1);
-  if (t >= pl.T) return;  // the whole wave exits
+  if (geo->atomic || t >= geo->T) return;  // the whole wave exits
   uint32_t* c = bf.counts + (size_t)t * pl.wgpg;
   uint32_t run = 0;
   // four 64-count blocks per step: their loads are issued before the first scan
@@ -456,8 +516,11 @@ __global__ __launch_bounds__(kBlock) void bwd_colscan_kernel(const BwdPlan pl, c
 // still gets one chunk, which writes its zeros), and fills the chunk -> tile table.
 __global__ __launch_bounds__(kPlanThreads) void bwd_plan_kernel(const BwdPlan pl, const BwdBuffers bf) {
   __shared__ uint32_t s_w[kPlanThreads / kWave];
-  const uint32_t per = (pl.T + kPlanThreads - 1) / kPlanThreads;
-  const uint32_t t0 = min(pl.T, threadIdx.x * per), t1 = min(pl.T, t0 + per);
+  const GeoP geo = geo_of(bf);
+  if (geo->atomic) return;
+  const uint32_t T = geo->T;
+  const uint32_t per = (T + kPlanThreads - 1) / kPlanThreads;
+  const uint32_t t0 = min(T, threadIdx.x * per), t1 = min(T, t0 + per);
   uint32_t sn = 0, sc = 0;
   for (uint32_t t = t0; t < t1; ++t) {
     const uint32_t n = bf.bin_start[t];
@@ -477,8 +540,8 @@ __global__ __launch_bounds__(kPlanThreads) void bwd_plan_kernel(const BwdPlan pl
     pc += nch;
   }
   if (threadIdx.x == 0) {
-    bf.bin_start[pl.T] = tot_n;
-    bf.chunk_off[pl.T] = tot_c;
+    bf.bin_start[T] = tot_n;
+    bf.chunk_off[T] = tot_c;
   }
 }
 
@@ -493,23 +556,26 @@ __global__ __launch_bounds__(kBlock) void bwd_fill_kernel(const BwdPlan pl, cons
   constexpr int RW = DIM + 2;
   constexpr int KP = kFillStage / kBlock;  // samples per thread per round
   extern __shared__ __attribute__((aligned(16))) uint32_t s_fill[];
+  const GeoP geo = geo_of(bf);
+  if (geo->atomic) return;
+  const int bins = geo->bins;
   uint32_t* s_rec = s_fill;                // [kFillStage * RW] records sorted by bin (16-byte aligned)
   uint32_t* s_dst = s_rec + kFillStage * RW;  // [kFillStage] global record index of each
   uint32_t* s_base = s_dst + kFillStage;   // [bins] next global record of each bin
-  uint32_t* s_cnt = s_base + pl.bins;      // [bins] round counts -> round offsets
-  uint32_t* s_w = s_cnt + pl.bins;         // [kBlock / kWave]
+  uint32_t* s_cnt = s_base + bins;         // [bins] round counts -> round offsets
+  uint32_t* s_w = s_cnt + bins;            // [kBlock / kWave]
   // 2D: a group's workgroups in a contiguous range per XCD, so its record lines are
   // written through one L2 (C2 fill 48 -> 44 us); 3D keeps them dealt round-robin
   // (C5 105 against 110 us grouped)
   const uint32_t lbk = DIM == 2 ? xcd_logical_block(blockIdx.x, gridDim.x) : blockIdx.x;
   const uint32_t g = lbk / (uint32_t)pl.wgpg;
   const uint32_t w = lbk - g * (uint32_t)pl.wgpg;
-  for (int i = threadIdx.x; i < pl.bins; i += kBlock)
-    s_base[i] = bf.bin_start[(size_t)g * pl.bins + i] + bf.counts[((size_t)g * pl.bins + i) * pl.wgpg + w];
+  for (int i = threadIdx.x; i < bins; i += kBlock)
+    s_base[i] = bf.bin_start[(size_t)g * bins + i] + bf.counts[((size_t)g * bins + i) * pl.wgpg + w];
   const uint32_t units = min((uint32_t)pl.upw, (pl.Q << pl.hg_log2) - w * (uint32_t)pl.upw);
   const int LP = pl.L * pl.P;
   for (int l = 0; l < pl.L; ++l) {
-    const BwdLevel& lv = pl.lv[l];
+    const BwdLevel lv = level_at(geo, l);
     const uint32_t lb0 = (uint32_t)lv.tile_off << pl.hg_log2;
     const uint32_t lb1 = (uint32_t)(lv.tile_off + lv.ntiles) << pl.hg_log2;
     const uint32_t n = units * (uint32_t)pl.P;
@@ -687,7 +753,9 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
 
   // Chunks are dealt to XCDs in contiguous ranges (workgroup i runs on XCD i % 8), so the
   // chunks of one (batch, head-group) share an XCD and its L2.
-  const uint32_t total = bf.chunk_off[pl.T];
+  const GeoP geo = geo_of(bf);
+  if (geo->atomic) return;
+  const uint32_t total = bf.chunk_off[geo->T];
   const uint32_t per = (total + kXcds - 1) / kXcds;
   const uint32_t slot = blockIdx.x / kXcds;
   if (slot >= per) return;
@@ -698,8 +766,8 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
   const uint32_t nch = bf.chunk_off[t + 1] - off;
   const uint32_t beg = bf.bin_start[t] + (c - off) * pl.R;
   const uint32_t end = min(bf.bin_start[t + 1], beg + pl.R);
-  const TileCoord tc = decode_tile(pl, t);
-  const BwdLevel lv = pl.lv[tc.l];
+  BwdLevel lv;
+  const TileCoord tc = decode_tile(pl, geo, t, &lv);
 
   const uint32_t S = pl.S;
   const uint32_t grow = (uint32_t)pl.C * 4u;  // bytes of one staged fp32 grad_out row
@@ -905,12 +973,17 @@ template <int DIM, typename EV, int VEC>
 __global__ __launch_bounds__(kBlock) void bwd_fold_kernel(const BwdPlan pl, const BwdBuffers bf) {
   typedef typename EV::T TV;
   // tiles in contiguous ranges per XCD, like the tile kernel's chunks, so most partials
-  // are read from the L2 that wrote them
-  const uint32_t t = xcd_logical_block(blockIdx.x, gridDim.x);
+  // are read from the L2 that wrote them (the grid may exceed the launch's tiles when it was
+  // sized without the shapes; the extra workgroups exit)
+  const GeoP geo = geo_of(bf);
+  const uint32_t T = geo->T;
+  if (geo->atomic || blockIdx.x >= T) return;
+  const uint32_t t = xcd_logical_block(blockIdx.x, T);
   const uint32_t off = bf.chunk_off[t];
   const uint32_t nch = bf.chunk_off[t + 1] - off;
-  const TileCoord tc = decode_tile(pl, t);
-  const BwdLevel lv = pl.lv[tc.l];
+  BwdLevel lv;
+  const TileCoord tc = decode_tile(pl, geo, t, &lv);
+  const uint32_t bins = (uint32_t)geo->bins;
   TV* gv = static_cast<TV*>(bf.grad_value);
   for (int i = threadIdx.x; i < pl.cells * pl.nvec; i += kBlock) {
     const int cell = (int)fdiv((uint32_t)i, pl.div_nvec), ch = i - cell * pl.nvec;
@@ -932,7 +1005,7 @@ __global__ __launch_bounds__(kBlock) void bwd_fold_kernel(const BwdPlan pl, cons
           (dz && (lz != 0 || tc.tz == 0)))
         continue;
       const int tibn = lv.tile_off + ((tc.tz - dz) * lv.nty + (tc.ty - dy)) * lv.ntx + (tc.tx - dx);
-      const uint32_t tn = tc.g * (uint32_t)pl.bins + (((uint32_t)tibn << pl.hg_log2) | tc.hsub);
+      const uint32_t tn = tc.g * bins + (((uint32_t)tibn << pl.hg_log2) | tc.hsub);
       const int rn = ((lz + dz * pl.TZ) * pl.RY + (ly + dy * pl.TY)) * pl.RX + (lx + dx * pl.TX);
       const uint32_t noff = bf.chunk_off[tn], nn = bf.chunk_off[tn + 1] - noff;
       add_partials<VEC>(o, bf.scratch + ((size_t)noff * pl.rcells + rn) * pl.C + ch * VEC,
@@ -943,50 +1016,75 @@ __global__ __launch_bounds__(kBlock) void bwd_fold_kernel(const BwdPlan pl, cons
   }
 }
 
+// ------------------------------------------------------------------ geometry
+// Device-resident shapes: the geometry computed from them on the device (one thread; at
+// most kMaxLevels levels).
+__global__ __launch_bounds__(kWave) void bwd_geom_kernel(const GeomArgs a, const int32_t* shapes,
+                                                         BwdGeom* dst) {
+  if (threadIdx.x == 0) make_geom(a, shapes, dst);
+}
+
 // ------------------------------------------------------------------ dispatch
 template <int DIM, typename EV, typename EC, int VEC>
-hipError_t run_bwd_t(const BwdPlan& pl, const BwdBuffers& bf, hipStream_t s) {
+hipError_t run_bwd_t(const BwdPlan& pl, const BwdGeom* host_geom, const GeomArgs* dev_args,
+                     const int32_t* dev_shapes, const BwdBuffers& bf, hipStream_t s) {
   const uint32_t nbin_wg = (uint32_t)pl.groups * (uint32_t)pl.wgpg;
-  const size_t hist_bytes = (size_t)pl.bins * sizeof(uint32_t);
+  const size_t hist_bytes = (size_t)pl.bins_cap * sizeof(uint32_t);
   if (nbin_wg == 0) return hipErrorInvalidValue;
-  if (pl.atomic) {
+  BwdGeom* geom = const_cast<BwdGeom*>(bf.geom);
+  // host shapes: the sample-gradient kernel gets the geometry as an argument and stores it
+  BwdPlan plx = pl;
+  plx.geom_arg = host_geom ? 1 : 0;
+  static const BwdGeom kNoGeom{};
+  const BwdGeom& hg = host_geom ? *host_geom : kNoGeom;
+  if (!host_geom)
+    hipLaunchKernelGGL(bwd_geom_kernel, dim3(1), dim3(kWave), 0, s, *dev_args, dev_shapes, geom);
+  if (pl.static_atomic || pl.fallback) {
+    // fp32 sums scattered with global atomics, then rounded once; with device shapes these
+    // kernels exit unless the geometry chose this path
     const uint32_t n = pl.value_bytes / (uint32_t)EV::kBytes;  // Bc * K * H * C
-    hipError_t e = launch_zero_bytes(bf.scratch, (size_t)n * sizeof(float), s);
-    if (e != hipSuccess) return e;
+    uint32_t zb = (n / 4 + kBlock - 1) / kBlock;
+    zb = zb < 1 ? 1 : (zb > 8192 ? 8192 : zb);
+    if (n) hipLaunchKernelGGL(bwd_clear_sums_kernel, dim3(zb), dim3(kBlock), 0, s, plx, bf, n);
     hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 0, -1, true>), dim3(nbin_wg),
-                       dim3(kGradThreads), 0, s, pl, bf);
-    uint32_t blocks = (n / VEC + kBlock - 1) / kBlock;
+                       dim3(kGradThreads), 0, s, plx, bf, hg);
+    uint32_t blocks = (uint32_t)((n / VEC + kBlock - 1) / kBlock);
+    if (pl.fallback) {
+      const uint64_t lb = (pl.grad_loc_elems + kBlock - 1) / kBlock;
+      blocks = blocks > lb ? blocks : (uint32_t)(lb < 8192 ? lb : 8192);
+    }
     blocks = blocks < 1 ? 1 : (blocks > 8192 ? 8192 : blocks);
-    if (n) hipLaunchKernelGGL((bwd_round_kernel<EV, VEC>), dim3(blocks), dim3(kBlock), 0, s,
-                              static_cast<const float*>(bf.scratch),
-                              static_cast<typename EV::T*>(bf.grad_value), n);
-    return hipGetLastError();
+    hipLaunchKernelGGL((bwd_round_kernel<EV, EC, VEC>), dim3(blocks), dim3(kBlock), 0, s, bf, n,
+                       pl.grad_loc_elems, DIM);
+    if (pl.static_atomic) return hipGetLastError();
   }
   // compile-time lane-group size for the common 16-byte lane loads of 4 or 8 lanes per unit
   if (pl.P == 4 && pl.coords_aligned && pl.lpu_log2 == 2)
     hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 4, 2>), dim3(nbin_wg), dim3(kGradThreads),
-                       hist_bytes, s, pl, bf);
+                       hist_bytes, s, plx, bf, hg);
   else if (pl.P == 4 && pl.coords_aligned && pl.lpu_log2 == 3)
     hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 4, 3>), dim3(nbin_wg), dim3(kGradThreads),
-                       hist_bytes, s, pl, bf);
+                       hist_bytes, s, plx, bf, hg);
   else if (pl.P == 8 && pl.coords_aligned && pl.lpu_log2 == 2)
     hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 8, 2>), dim3(nbin_wg), dim3(kGradThreads),
-                       hist_bytes, s, pl, bf);
+                       hist_bytes, s, plx, bf, hg);
   else if (pl.P == 8 && pl.coords_aligned && pl.lpu_log2 == 3)
     hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 8, 3>), dim3(nbin_wg), dim3(kGradThreads),
-                       hist_bytes, s, pl, bf);
+                       hist_bytes, s, plx, bf, hg);
   else if (pl.P == 4 && pl.coords_aligned)
     hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 4, -1>), dim3(nbin_wg), dim3(kGradThreads),
-                       hist_bytes, s, pl, bf);
+                       hist_bytes, s, plx, bf, hg);
   else if (pl.P == 8 && pl.coords_aligned)
     hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 8, -1>), dim3(nbin_wg), dim3(kGradThreads),
-                       hist_bytes, s, pl, bf);
+                       hist_bytes, s, plx, bf, hg);
   else
     hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 0, -1>), dim3(nbin_wg), dim3(kGradThreads),
-                       hist_bytes, s, pl, bf);
-  if (pl.T == 0) return hipGetLastError();  // no cell in any level: grad_value is empty
+                       hist_bytes, s, plx, bf, hg);
+  if (pl.T_cap == 0) return hipGetLastError();  // no cell in any level: grad_value is empty
+  // grids sized by T_cap (the launch's tiles when the host knows the shapes, an upper bound
+  // otherwise); workgroups beyond the geometry's T exit
   const uint32_t waves_per_block = kBlock / kWave;
-  hipLaunchKernelGGL(bwd_colscan_kernel, dim3((pl.T + waves_per_block - 1) / waves_per_block),
+  hipLaunchKernelGGL(bwd_colscan_kernel, dim3((pl.T_cap + waves_per_block - 1) / waves_per_block),
                      dim3(kBlock), 0, s, pl, bf);
   hipLaunchKernelGGL(bwd_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, pl, bf);
   const size_t fill_bytes = 2 * hist_bytes +
@@ -995,11 +1093,12 @@ hipError_t run_bwd_t(const BwdPlan& pl, const BwdBuffers& bf, hipStream_t s) {
   hipLaunchKernelGGL((bwd_fill_kernel<DIM, EC>), dim3(nbin_wg), dim3(kBlock), fill_bytes, s, pl, bf);
   hipLaunchKernelGGL((bwd_tile_kernel<DIM, EV, EC, VEC>), dim3(pl.grid_chunks),
                      dim3(kTileThreads<DIM>), pl.lds_bytes, s, pl, bf);
-  hipLaunchKernelGGL((bwd_fold_kernel<DIM, EV, VEC>), dim3(pl.T), dim3(kBlock), 0, s, pl, bf);
+  hipLaunchKernelGGL((bwd_fold_kernel<DIM, EV, VEC>), dim3(pl.T_cap), dim3(kBlock), 0, s, pl, bf);
   return hipGetLastError();
 }
 
-using BwdFn = hipError_t (*)(const BwdPlan&, const BwdBuffers&, hipStream_t);
+using BwdFn = hipError_t (*)(const BwdPlan&, const BwdGeom*, const GeomArgs*, const int32_t*,
+                             const BwdBuffers&, hipStream_t);
 
 template <int DIM, typename EV, typename EC>
 BwdFn pick_vec(int vec_bytes) {
@@ -1057,28 +1156,32 @@ bool bwd_supported(int dim, int vdt, int cdt, int vec_bytes) {
 
 BwdSizes bwd_sizes(const BwdPlan& pl, uint64_t samples, int dim) {
   BwdSizes z;
-  z.counts = (uint64_t)pl.groups * pl.wgpg * pl.bins;
-  z.bin_start = (uint64_t)pl.T + 1;
-  z.chunk_off = (uint64_t)pl.T + 1;
+  const bool binned = !pl.static_atomic;
+  const bool sums = pl.static_atomic || pl.fallback;
+  z.counts = binned ? (uint64_t)pl.groups * pl.wgpg * pl.bins_cap : 0u;
+  z.bin_start = (uint64_t)pl.T_cap + 1;
+  z.chunk_off = (uint64_t)pl.T_cap + 1;
   z.chunk_tile = pl.max_chunks;
-  z.record_words = pl.atomic ? 0u : (samples > 0 ? samples : 1) * (uint64_t)(dim + 2);
-  // atomic plans: one fp32 sum per grad_value element of a launch (groups << hg_log2 =
+  z.record_words = binned ? (samples > 0 ? samples : 1) * (uint64_t)(dim + 2) : 0u;
+  z.scratch_floats = binned ? (uint64_t)pl.max_chunks * pl.rcells * pl.C : 0u;
+  // atomic path: one fp32 sum per grad_value element of a launch (groups << hg_log2 =
   // batches * H)
-  z.scratch_floats = pl.atomic ? ((uint64_t)pl.groups << pl.hg_log2) * (uint64_t)pl.K * pl.C
-                               : (uint64_t)pl.max_chunks * pl.rcells * pl.C;
+  z.sum_floats = sums ? ((uint64_t)pl.groups << pl.hg_log2) * (uint64_t)pl.K * pl.C : 0u;
   z.value_h_bytes = pl.head_major ? (uint64_t)pl.value_bytes : 0u;
+  z.geom_bytes = sizeof(BwdGeom);
   auto al = [](uint64_t b) { return (b + 255) & ~(uint64_t)255; };
   z.total_bytes = al(z.counts * 4) + al(z.bin_start * 4) + al(z.chunk_off * 4) +
                   al(z.chunk_tile * 4) + al(z.record_words * 4) + al(z.scratch_floats * 4) +
-                  al(z.value_h_bytes);
+                  al(z.sum_floats * 4) + al(z.value_h_bytes) + al(z.geom_bytes);
   return z;
 }
 
-hipError_t run_bwd(const BwdPlan& pl, const BwdBuffers& bf, int dim, int vdt, int cdt,
+hipError_t run_bwd(const BwdPlan& pl, const BwdGeom* host_geom, const GeomArgs* dev_args,
+                   const int32_t* dev_shapes, const BwdBuffers& bf, int dim, int vdt, int cdt,
                    int vec_bytes, hipStream_t s) {
   BwdFn fn = get_bwd(dim, vdt, cdt, vec_bytes);
-  if (!fn) return hipErrorInvalidValue;
-  return fn(pl, bf, s);
+  if (!fn || (!host_geom && (!dev_args || !dev_shapes))) return hipErrorInvalidValue;
+  return fn(pl, host_geom, dev_args, dev_shapes, bf, s);
 }
 
 }  // namespace msda

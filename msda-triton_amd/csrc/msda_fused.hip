@@ -51,6 +51,14 @@ struct SumOp {
   __device__ float operator()(float a, float b) const { return a + b; }
 };
 
+// 1 / extent of level l along axis d (x: W, y: H, z: D), fp32 and correctly rounded: from
+// the device shapes when the host has none, with the fused forward's division.
+template <int DIM>
+__device__ inline float inv_at(const FusedArgs& a, uint32_t l, int d) {
+  if (a.shapes) return 1.0f / (float)a.shapes[l * DIM + (DIM - 1 - d)];
+  return a.inv[l][d];
+}
+
 // loc of sample i (unit u, sample j of the unit, level l) from its offsets and the
 // reference point of (b, q, l)
 template <int DIM, typename EI>
@@ -59,7 +67,7 @@ __device__ inline void form_loc(const FusedArgs& a, uint32_t i, uint32_t u, uint
   const float* r = a.ref + (bq * (uint32_t)a.L + l) * DIM;
 #pragma unroll
   for (int d = 0; d < DIM; ++d)
-    a.loc[i * DIM + d] = __builtin_fmaf(ld<EI>(a.off, i * DIM + d), a.inv[l][d], r[d]);
+    a.loc[i * DIM + d] = __builtin_fmaf(ld<EI>(a.off, i * DIM + d), inv_at<DIM>(a, l, d), r[d]);
 }
 
 template <int DIM, typename EI>
@@ -114,7 +122,7 @@ __global__ __launch_bounds__(kBlock) void fused_grad_kernel(const FusedArgs a) {
       st<EI>(a.grad_logits, i, at * (ga - dot));
       const uint32_t l = j / (uint32_t)a.P;
 #pragma unroll
-      for (int d = 0; d < DIM; ++d) st<EI>(a.grad_off, i * DIM + d, a.grad_loc[i * DIM + d] * a.inv[l][d]);
+      for (int d = 0; d < DIM; ++d) st<EI>(a.grad_off, i * DIM + d, a.grad_loc[i * DIM + d] * inv_at<DIM>(a, l, d));
       return;
     }
     const uint32_t o = t * LP;
@@ -125,7 +133,7 @@ __global__ __launch_bounds__(kBlock) void fused_grad_kernel(const FusedArgs a) {
       const uint32_t l = s / (uint32_t)a.P;
 #pragma unroll
       for (int d = 0; d < DIM; ++d)
-        st<EI>(a.grad_off, (o + s) * DIM + d, a.grad_loc[(o + s) * DIM + d] * a.inv[l][d]);
+        st<EI>(a.grad_off, (o + s) * DIM + d, a.grad_loc[(o + s) * DIM + d] * inv_at<DIM>(a, l, d));
     }
     return;
   }

@@ -114,8 +114,94 @@ struct BwdLevel {
   int32_t sy, sz;              // byte strides along y and z (W * rs, H * W * rs); x is rs
 };
 
-struct BwdPlan {
+// Level geometry of one backward launch: what depends on the level shapes. It lives in
+// the workspace and the kernels read it through a constant-address-space pointer, so a
+// wave-uniform field is one scalar load, as a kernel argument would be. Host-resident
+// shapes: computed on the host and passed to the sample-gradient kernel, which stores it.
+// Device-resident shapes: computed by bwd_geom_kernel from the shapes on the device, so the
+// host never reads them (no device-to-host copy, no synchronisation; the launch sequence
+// can be graph-captured).
+struct BwdGeom {
   BwdLevel lv[kMaxLevels];
+  int32_t tiles_per_bh;        // tiles of all levels of one (b, h)
+  int32_t bins;                // tiles_per_bh * HG; bin = tile_in_bh * HG + head_in_group
+  uint32_t T;                  // groups * bins: tiles of this launch
+  int32_t mul24;               // every row stride and corner index fits 24-bit multiplies
+  int32_t atomic;              // grad_value goes through fp32 atomics into BwdBuffers::sums
+                               // (levels beyond the binning capacity, or invalid shapes)
+  int32_t invalid;             // device shapes disagree with K (or overflow 32-bit offsets):
+                               // every gradient is filled with NaN
+  int32_t pad[2];
+};
+
+// Inputs of make_geom besides the shapes (all known on the host without the shapes).
+struct GeomArgs {
+  int32_t dim, L, H, C, s;     // s = bytes per value element
+  int32_t head_major;          // rows of one head contiguous (head-major value copy)
+  int32_t hg_log2, groups;
+  int32_t TX, TY, TZ;
+  int32_t bins_cap;            // bins the launch was sized for; more -> atomic path
+  int32_t static_atomic;       // the host already chose the atomic path
+  int64_t K;
+};
+
+// Tiles along one axis of extent n for tiles of t cells.
+__host__ __device__ inline int32_t tiles_along(int32_t n, int32_t t) { return (n + t - 1) / t; }
+
+// The level geometry of a launch from the (L, dim) int32 shapes (rows (H, W) or (D, H, W)).
+// Shared by the host planner and bwd_geom_kernel so both paths compute the same table.
+__host__ __device__ inline void make_geom(const GeomArgs& a, const int32_t* hs, BwdGeom* g) {
+  int64_t total = 0;
+  bool bad = false;
+  const uint64_t rsb = (uint64_t)(a.head_major ? 1 : a.H) * a.C * a.s;  // bytes between rows of K
+  bool mul24 = rsb < (1u << 23);
+  int32_t tiles = 0;
+  for (int l = 0; l < a.L; ++l) {
+    BwdLevel& lv = g->lv[l];
+    const int32_t d0 = hs[l * a.dim], d1 = hs[l * a.dim + 1];
+    const int32_t d2 = a.dim == 3 ? hs[l * a.dim + 2] : 1;
+    lv.D = a.dim == 3 ? d0 : 1;
+    lv.H = a.dim == 3 ? d1 : d0;
+    lv.W = a.dim == 3 ? d2 : d1;
+    if (lv.D < 0 || lv.H < 0 || lv.W < 0) bad = true;
+    lv.start = (int32_t)total;
+    if (!bad) total += (int64_t)lv.D * lv.H * lv.W;
+    if (total > 0x7FFFFFFFll) bad = true;
+  }
+  if (total != a.K) bad = true;
+  for (int l = a.L - 1; l >= 0; --l) {  // coarsest level first: its chunks are the longest
+    BwdLevel& lv = g->lv[l];
+    if (bad) {
+      lv = BwdLevel{};
+      continue;
+    }
+    lv.base = (uint32_t)((uint64_t)lv.start * rsb);
+    lv.sy = (int32_t)((uint64_t)lv.W * rsb);
+    lv.sz = (int32_t)((uint64_t)lv.W * lv.H * rsb);
+    // largest stride used (y in 2D, z in 3D) and largest corner index must fit 24 bits
+    const uint64_t top = (uint64_t)lv.W * (a.dim == 3 ? (uint64_t)lv.H : 1u) * rsb;
+    const int64_t ext = (lv.W > lv.H ? (lv.W > lv.D ? lv.W : lv.D) : (lv.H > lv.D ? lv.H : lv.D)) + 2;
+    if (top >= (1u << 23) || ext >= (1 << 23)) mul24 = false;
+    lv.ntx = tiles_along(lv.W, a.TX);
+    lv.nty = tiles_along(lv.H, a.TY);
+    lv.ntz = tiles_along(lv.D, a.TZ);
+    lv.tile_off = tiles;
+    const int64_t nt = a.static_atomic ? 0 : (int64_t)lv.ntx * lv.nty * lv.ntz;
+    lv.ntiles = (int32_t)(nt < 0x40000000 ? nt : 0x40000000);
+    tiles = tiles + lv.ntiles < 0x40000000 ? tiles + lv.ntiles : 0x40000000;
+  }
+  const int64_t bins = (int64_t)tiles << a.hg_log2;
+  const bool over = bins > a.bins_cap;
+  g->tiles_per_bh = over || bad ? 0 : tiles;
+  g->bins = over || bad ? 0 : (int32_t)bins;
+  g->T = (uint32_t)a.groups * (uint32_t)g->bins;
+  g->mul24 = mul24 && !bad ? 1 : 0;
+  g->atomic = (a.static_atomic || over || bad) ? 1 : 0;
+  g->invalid = bad ? 1 : 0;
+  g->pad[0] = g->pad[1] = 0;
+}
+
+struct BwdPlan {
   int32_t L, P, C, H, K;
   uint32_t Q;
   FastDiv div_p;               // divisor P (record id -> q, p)
@@ -130,29 +216,33 @@ struct BwdPlan {
   int32_t RX, RY, RZ;          // region: tile + 1 along each axis (RZ = 1 in 2D)
   int32_t cells;               // owned cells per tile: TX * TY * TZ
   int32_t rcells;              // region cells per tile: RX * RY * RZ
-  int32_t tiles_per_bh;
   int32_t hg_log2;
   int32_t groups;              // (batches in launch) * H / HG
   int32_t upw;                 // units (b, q, h) per bin workgroup: rounds * kGradThreads / lanes per unit
   int32_t wgpg;                // bin workgroups per group: ceil(Q * HG / upw)
-  int32_t bins;                // tiles_per_bh * HG; bin = tile_in_bh * HG + head_in_group
-  uint32_t T;                  // groups * bins: tiles of this launch
+  int32_t bins_cap;            // bins the LDS histograms and the count matrix are sized for
+  uint32_t T_cap;              // groups * bins_cap: tiles the tables and grids are sized for
   uint32_t R;                  // records per chunk (multiple of S)
   uint32_t S;                  // records per LDS sub-batch of the tile kernel (<= kTileThreads<DIM>)
   int32_t lpu_log2, nvec;
   int32_t clamp;
   int32_t coords_aligned;      // loc and attn are 16-byte aligned: per-batch block loads allowed
-  int32_t mul24;               // every row stride and corner index fits 24-bit multiplies
   int32_t head_major;          // the sample-gradient kernel reads BwdBuffers::value_h
-  int32_t atomic;              // levels exceed the LDS binning (more than kMaxBinsLds tiles per
-                               // head): grad_value is scattered with fp32 atomics into
-                               // BwdBuffers::scratch, then rounded into grad_value
+  int32_t static_atomic;       // the host chose the atomic path (levels beyond the LDS binning,
+                               // or sample ids beyond a record): grad_value is scattered with
+                               // fp32 atomics into BwdBuffers::sums, then rounded into grad_value
+  int32_t fallback;            // device shapes: the binned and the atomic kernels are both
+                               // launched and each exits unless BwdGeom::atomic selects it
+  int32_t geom_arg;            // host shapes: the sample-gradient kernel (the first to need the
+                               // geometry) reads it from its kernel argument and stores it in
+                               // the workspace for the kernels after it
   float lo_g, hi_g;
   uint32_t value_bytes;
   uint32_t lds_g_bytes;        // bytes of the staged fp32 grad_out rows of a sub-batch
   uint32_t lds_bytes;          // total dynamic LDS of the tile kernel
   uint32_t max_chunks;         // upper bound of the chunk count
   uint32_t grid_chunks;        // tile-kernel grid: max_chunks rounded up to 8 (one per XCD)
+  uint64_t grad_loc_elems;     // Bc * Q * H * L * P * dim (NaN fill of invalid shapes)
 };
 
 struct BwdBuffers {
@@ -169,12 +259,15 @@ struct BwdBuffers {
   uint32_t* chunk_off;   // T + 1: first chunk of each tile; [T] = number of chunks
   uint32_t* chunk_tile;  // max_chunks: tile of each chunk
   uint32_t* records;     // (DIM + 2) words per record: id | flags, u_x, u_y[, u_z], attn
-  float* scratch;        // max_chunks * rcells * C fp32 partials; atomic plans: (Bc, K, H, C) fp32 sums
+  float* scratch;        // max_chunks * rcells * C fp32 partials
+  float* sums;           // atomic path: (Bc, K, H, C) fp32 sums
+  const BwdGeom* geom;   // level geometry of the launch (written by the first kernel)
 };
 
 struct BwdSizes {
-  uint64_t counts, bin_start, chunk_off, chunk_tile, record_words, scratch_floats;
+  uint64_t counts, bin_start, chunk_off, chunk_tile, record_words, scratch_floats, sum_floats;
   uint64_t value_h_bytes;  // head-major value copy (0 when the plan does not use one)
+  uint64_t geom_bytes;
   uint64_t total_bytes;
 };
 
@@ -184,8 +277,11 @@ BwdSizes bwd_sizes(const BwdPlan& pl, uint64_t samples, int dim);
 // Clear `bytes` bytes of device memory with a fill kernel (no hipMemset node in graphs).
 hipError_t launch_zero_bytes(void* p, size_t bytes, hipStream_t s);
 
-// Enqueue the whole backward for one launch (batch range) on stream s.
-hipError_t run_bwd(const BwdPlan& pl, const BwdBuffers& bf, int dim, int vdt, int cdt,
+// Enqueue the whole backward for one launch (batch range) on stream s. Its first kernel
+// writes bf.geom: a copy of *host_geom, or (host_geom == nullptr) make_geom(*dev_args,
+// dev_shapes) computed on the device.
+hipError_t run_bwd(const BwdPlan& pl, const BwdGeom* host_geom, const GeomArgs* dev_args,
+                   const int32_t* dev_shapes, const BwdBuffers& bf, int dim, int vdt, int cdt,
                    int vec_bytes, hipStream_t s);
 
 bool bwd_supported(int dim, int vdt, int cdt, int vec_bytes);
@@ -209,6 +305,8 @@ struct FusedArgs {
   int32_t H, L, P;
   int32_t g_log2;           // lanes per unit = 2^g_log2 >= L * P (<= 64), or -1: one thread per unit
   float inv[kMaxLevels][3];   // 1/W, 1/H, 1/D per level (fp32, correctly rounded)
+  const int32_t* shapes;    // device (L, dim) shapes, or nullptr: the kernels then compute the
+                            // reciprocals from them (as the fused forward does) instead of inv
 };
 
 // grad == false: loc and attn from ref, off and logits. grad == true: grad_ref, grad_off and

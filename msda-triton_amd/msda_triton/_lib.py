@@ -12,7 +12,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libmsda_hip.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 MSDA_F32, MSDA_F16, MSDA_BF16 = 0, 1, 2
 MSDA_OK, MSDA_ERR_INVALID, MSDA_ERR_DTYPE, MSDA_ERR_WORKSPACE, MSDA_ERR_HIP = range(5)
@@ -25,9 +25,13 @@ EXPORTED_SYMBOLS = (
     "msda_fwd",
     "msda_bwd_workspace_bytes",
     "msda_bwd",
+    "msda_bwd_dev_workspace_bytes",
+    "msda_bwd_dev",
     "msda_fwd_fused",
     "msda_bwd_fused_workspace_bytes",
     "msda_bwd_fused",
+    "msda_bwd_fused_dev_workspace_bytes",
+    "msda_bwd_fused_dev",
 )
 
 
@@ -87,6 +91,10 @@ def load() -> ctypes.CDLL:
         lib.msda_bwd_workspace_bytes.restype = ctypes.c_size_t
         lib.msda_bwd.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, vp, ctypes.c_size_t, vp]
         lib.msda_bwd.restype = ctypes.c_int
+        lib.msda_bwd_dev_workspace_bytes.argtypes = [dp]
+        lib.msda_bwd_dev_workspace_bytes.restype = ctypes.c_size_t
+        lib.msda_bwd_dev.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, vp, ctypes.c_size_t, vp]
+        lib.msda_bwd_dev.restype = ctypes.c_int
         lib.msda_fwd_fused.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, ctypes.c_size_t, vp]
         lib.msda_fwd_fused.restype = ctypes.c_int
         lib.msda_bwd_fused_workspace_bytes.argtypes = [dp, vp]
@@ -94,6 +102,11 @@ def load() -> ctypes.CDLL:
         lib.msda_bwd_fused.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp,
                                        ctypes.c_size_t, vp]
         lib.msda_bwd_fused.restype = ctypes.c_int
+        lib.msda_bwd_fused_dev_workspace_bytes.argtypes = [dp]
+        lib.msda_bwd_fused_dev_workspace_bytes.restype = ctypes.c_size_t
+        lib.msda_bwd_fused_dev.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp,
+                                           ctypes.c_size_t, vp]
+        lib.msda_bwd_fused_dev.restype = ctypes.c_int
         version = lib.msda_abi_version()
         if version != ABI_VERSION:
             raise RuntimeError(

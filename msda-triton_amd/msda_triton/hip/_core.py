@@ -82,34 +82,17 @@ def validate_inputs(name: str, dim: int, value: torch.Tensor, value_spatial_shap
 
 class Levels:
     """Level tables of one call: (L, dim) int32 shapes and (L,) int32 starts on the device
-    (read by the forward kernel) and a host (L, dim) int32 copy of the shapes (planned from
-    by the backward). For GPU-resident shapes the host copy arrives asynchronously in pinned
-    memory; ``host()`` waits for it."""
+    (read by the forward kernel) and, for CPU-resident shapes, a host (L, dim) int32 copy of
+    the shapes (planned from by the backward). GPU-resident shapes have no host copy: their
+    backward (msda_bwd_dev) derives its plan from the device tables on the device, so no
+    call ever waits for the device."""
 
-    __slots__ = ("spatial", "starts", "_host", "_event")
+    __slots__ = ("spatial", "starts", "host")
 
-    def __init__(self, spatial, starts, host, event=None):
+    def __init__(self, spatial, starts, host):
         self.spatial = spatial
         self.starts = starts
-        self._host = host
-        self._event = event
-
-    def start_host_copy(self) -> None:
-        """Begin the asynchronous device-to-host copy of the shapes (GPU-resident shapes
-        only; the backward plans from the host copy)."""
-        if self._host is None:
-            host = torch.empty(self.spatial.shape, dtype=torch.int32, pin_memory=True)
-            host.copy_(self.spatial, non_blocking=True)
-            event = torch.cuda.Event()
-            event.record(torch.cuda.current_stream(self.spatial.device))
-            self._host, self._event = host, event
-
-    def host(self) -> torch.Tensor:
-        self.start_host_copy()
-        if self._event is not None:
-            self._event.synchronize()
-            self._event = None
-        return self._host
+        self.host = host
 
 
 def prepare_levels(dim: int, value: torch.Tensor, value_spatial_shapes: torch.Tensor) -> Levels:
@@ -118,8 +101,7 @@ def prepare_levels(dim: int, value: torch.Tensor, value_spatial_shapes: torch.Te
     CPU-resident shapes are checked against K and the int32 range (as in
     _prepare_spatial_2d, triton/msda_2d.py:53-74) and their device copy is cached.
     GPU-resident shapes are converted on the device without a host sync and without the
-    K check (triton/msda_2d.py:76-82), cached for the live, unmodified tensor; their host
-    copy (needed by the backward only) starts with Levels.start_host_copy().
+    K check (triton/msda_2d.py:76-82), cached for the live, unmodified tensor.
     """
     device = value.device
     if value_spatial_shapes.device.type == "cpu":
@@ -298,17 +280,25 @@ def backward(dim: int, grad_output: torch.Tensor, value_c: torch.Tensor, levels:
     grad_loc = torch.empty(loc_c.shape, device=loc_c.device, dtype=loc_c.dtype)
     grad_attn = torch.empty(attn_c.shape, device=attn_c.device, dtype=attn_c.dtype)
     desc = make_desc(dim, value_c, loc_c, loc_c.dtype, clamp_grid, clamp_eps)
-    host = levels.host()
-    ws_bytes = int(lib.msda_bwd_workspace_bytes(ctypes.byref(desc), host.data_ptr()))
+    if levels.host is not None:
+        # CPU-resident shapes: the host plans every size exactly
+        name, shapes = "msda_bwd", levels.host.data_ptr()
+        ws_bytes = int(lib.msda_bwd_workspace_bytes(ctypes.byref(desc), shapes))
+        entry = lib.msda_bwd
+    else:
+        # GPU-resident shapes: the plan is derived on the device (no host read, no sync)
+        name, shapes = "msda_bwd_dev", levels.spatial.data_ptr()
+        ws_bytes = int(lib.msda_bwd_dev_workspace_bytes(ctypes.byref(desc)))
+        entry = lib.msda_bwd_dev
     if ws_bytes == 0 and _lib.last_error():
-        _lib.check(_lib.MSDA_ERR_INVALID, "msda_bwd_workspace_bytes")
+        _lib.check(_lib.MSDA_ERR_INVALID, name + "_workspace_bytes")
     ws = torch.empty(max(ws_bytes, 1), device=value_c.device, dtype=torch.uint8)
     with _on_device(value_c.device):
-        rc = lib.msda_bwd(ctypes.byref(desc), host.data_ptr(), value_c.data_ptr(),
-                          loc_c.data_ptr(), attn_c.data_ptr(), grad_out.data_ptr(),
-                          grad_value.data_ptr(), grad_loc.data_ptr(), grad_attn.data_ptr(),
-                          ws.data_ptr(), ws_bytes, _stream(value_c.device))
-    _lib.check(rc, "msda_bwd")
+        rc = entry(ctypes.byref(desc), shapes, value_c.data_ptr(), loc_c.data_ptr(),
+                   attn_c.data_ptr(), grad_out.data_ptr(), grad_value.data_ptr(),
+                   grad_loc.data_ptr(), grad_attn.data_ptr(), ws.data_ptr(), ws_bytes,
+                   _stream(value_c.device))
+    _lib.check(rc, name)
     return grad_value, grad_loc, grad_attn
 
 
@@ -317,7 +307,6 @@ def fn_forward(ctx, name: str, dim: int, value, value_spatial_shapes, sampling_l
     """Body of MSDA2DFn.forward / MSDA3DFn.forward (reference triton/msda_2d.py:749-775)."""
     validate_inputs(name, dim, value, value_spatial_shapes, sampling_locations, attention_weights)
     levels = prepare_levels(dim, value, value_spatial_shapes)
-    levels.start_host_copy()  # the backward plans from it; overlap the copy with the forward
     out, value_c, loc_c, attn_c = forward(dim, value, levels, sampling_locations,
                                           attention_weights, clamp_grid, clamp_eps)
     ctx.save_for_backward(value_c, loc_c, attn_c)

@@ -112,18 +112,22 @@ def backward(dim: int, grad_output, value_c, levels, ref_c, off_c, logits_c, cla
     grad_off = torch.empty(off_c.shape, device=off_c.device, dtype=off_c.dtype)
     grad_logits = torch.empty(logits_c.shape, device=logits_c.device, dtype=logits_c.dtype)
     desc = _desc(dim, value_c, off_c, off_c.dtype, clamp_grid, clamp_eps)
-    host = levels.host()
-    ws_bytes = int(lib.msda_bwd_fused_workspace_bytes(ctypes.byref(desc), host.data_ptr()))
+    if levels.host is not None:
+        name, shapes, entry = "msda_bwd_fused", levels.host.data_ptr(), lib.msda_bwd_fused
+        ws_bytes = int(lib.msda_bwd_fused_workspace_bytes(ctypes.byref(desc), shapes))
+    else:
+        # GPU-resident shapes: planned on the device, no host read of the shapes
+        name, shapes, entry = "msda_bwd_fused_dev", levels.spatial.data_ptr(), lib.msda_bwd_fused_dev
+        ws_bytes = int(lib.msda_bwd_fused_dev_workspace_bytes(ctypes.byref(desc)))
     if ws_bytes == 0 and _lib.last_error():
-        _lib.check(_lib.MSDA_ERR_INVALID, "msda_bwd_fused_workspace_bytes")
+        _lib.check(_lib.MSDA_ERR_INVALID, name + "_workspace_bytes")
     ws = torch.empty(max(ws_bytes, 1), device=value_c.device, dtype=torch.uint8)
     with _core._on_device(value_c.device):
-        rc = lib.msda_bwd_fused(ctypes.byref(desc), host.data_ptr(), value_c.data_ptr(),
-                                ref_c.data_ptr(), off_c.data_ptr(), logits_c.data_ptr(),
-                                grad_out.data_ptr(), grad_value.data_ptr(), grad_ref.data_ptr(),
-                                grad_off.data_ptr(), grad_logits.data_ptr(), ws.data_ptr(),
-                                ws_bytes, _core._stream(value_c.device))
-    _lib.check(rc, "msda_bwd_fused")
+        rc = entry(ctypes.byref(desc), shapes, value_c.data_ptr(), ref_c.data_ptr(),
+                   off_c.data_ptr(), logits_c.data_ptr(), grad_out.data_ptr(),
+                   grad_value.data_ptr(), grad_ref.data_ptr(), grad_off.data_ptr(),
+                   grad_logits.data_ptr(), ws.data_ptr(), ws_bytes, _core._stream(value_c.device))
+    _lib.check(rc, name)
     return grad_value, grad_ref, grad_off, grad_logits
 
 
@@ -137,7 +141,6 @@ class MSDAFusedFn(torch.autograd.Function):
         logits, ref = validate_fused_inputs(name, dim, value, value_spatial_shapes,
                                             reference_points, sampling_offsets, attention_logits)
         levels = _core.prepare_levels(dim, value, value_spatial_shapes)
-        levels.start_host_copy()
         out, value_c, ref_c, off_c, logits_c = forward(dim, value, levels, ref, sampling_offsets,
                                                        logits, clamp_grid, clamp_eps)
         ctx.save_for_backward(value_c, ref_c, off_c, logits_c)

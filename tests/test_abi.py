@@ -207,7 +207,7 @@ def test_prepare_levels_cpu_shape_checks():
         _core.prepare_levels(2, value, torch.tensor([[65536, 65536]]))
     lv = _core.prepare_levels(2, torch.zeros(1, 13, 1, 4), torch.tensor([[3, 3], [2, 2]]))
     assert lv.starts.tolist() == [0, 9]
-    assert lv.host().tolist() == [[3, 3], [2, 2]]
+    assert lv.host.tolist() == [[3, 3], [2, 2]]
 
 
 def test_public_api_surface():
