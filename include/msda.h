@@ -285,6 +285,32 @@ int msda_bwd_fused_dev(const msda_desc* desc,
                        size_t workspace_bytes,
                        void* stream);
 
+/* Bytes of the static device scratch msda_bwd_noalloc uses as its workspace (256 MiB per GPU). */
+#define MSDA_NOALLOC_SCRATCH_BYTES ((size_t)256 << 20)
+
+/*
+ * msda_bwd that allocates nothing: no counterpart in the reference. It is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Arguments and results are those of msda_bwd, without
+ * the workspace: the workspace is a static device array of MSDA_NOALLOC_SCRATCH_BYTES that
+ * each GPU the library runs on holds from module load until the process ends, its device
+ * address looked up once per device on the first call there. A problem whose
+ * msda_bwd_workspace_bytes() exceeds that size is refused with MSDA_ERR_WORKSPACE (the
+ * 2D encoder workload, B=2 Q=K=19947, needs about 165 MB; the 3D 4-level one, about
+ * 600 MB, does not fit). Every call on one GPU shares that GPU's array: calls that overlap
+ * on one GPU (other streams or threads) race, so callers serialise them.
+ */
+int msda_bwd_noalloc(const msda_desc* desc,
+                     const int32_t* host_spatial_shapes,
+                     const void* value,
+                     const void* sampling_locations,
+                     const void* attention_weights,
+                     const void* grad_output,
+                     void* grad_value,
+                     void* grad_sampling_locations,
+                     void* grad_attention_weights,
+                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif

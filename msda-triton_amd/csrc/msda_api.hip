@@ -702,6 +702,18 @@ int fused_bwd_impl(const msda_desc* d, const int32_t* hs, const int32_t* ds, con
 
 }  // namespace
 
+namespace msda {
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+}  // namespace msda
+
 extern "C" {
 
 int msda_abi_version(void) { return MSDA_ABI_VERSION; }

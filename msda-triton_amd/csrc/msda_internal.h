@@ -286,6 +286,9 @@ hipError_t run_bwd(const BwdPlan& pl, const BwdGeom* host_geom, const GeomArgs* 
 
 bool bwd_supported(int dim, int vdt, int cdt, int vec_bytes);
 
+// Set the thread-local text msda_last_error() returns (printf format) and return `code`.
+int set_error(int code, const char* fmt, ...);
+
 // ---------------------------------------------------------------------------------------
 // Producer-side kernels of the fused path's backward (msda_fused.hip), for one launch over
 // a batch range (units * L * P * 2^dim < 2^31).

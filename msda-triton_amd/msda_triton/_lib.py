@@ -32,7 +32,9 @@ EXPORTED_SYMBOLS = (
     "msda_bwd_fused",
     "msda_bwd_fused_dev_workspace_bytes",
     "msda_bwd_fused_dev",
+    "msda_bwd_noalloc",
 )
+NOALLOC_SCRATCH_BYTES = 256 << 20  # MSDA_NOALLOC_SCRATCH_BYTES
 
 
 class MsdaDesc(ctypes.Structure):
@@ -107,6 +109,8 @@ def load() -> ctypes.CDLL:
         lib.msda_bwd_fused_dev.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp,
                                            ctypes.c_size_t, vp]
         lib.msda_bwd_fused_dev.restype = ctypes.c_int
+        lib.msda_bwd_noalloc.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+        lib.msda_bwd_noalloc.restype = ctypes.c_int
         version = lib.msda_abi_version()
         if version != ABI_VERSION:
             raise RuntimeError(
