@@ -12,8 +12,15 @@ HBM. Algorithmic bytes, s = element size: V = B*K*H*C*s, G = B*Q*H*L*P*2^d*C*s,
 S = B*Q*H*L*P*d*s, A = B*Q*H*L*P*s, O = B*Q*H*C*s, V' = min(V, G);
 fwd = V' + S + A + O, bwd = 2V' + 2S + 2A + O.
 
+Beside the warm (back-to-back) times, each workload is also timed MALL-flushed (a 512 MiB
+buffer written between iterations, outside the timed events; median of per-iteration times)
+and, for fwd+bwd, the reference benchmark's way (inputs cloned and grad_output drawn with
+randn_like inside the timed region, benchmarks/benchmark_msda2d.py:210-218).
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
        python bench.py --mode copy   (plain copy kernel of known size, for PMC calibration)
+       python bench.py --mode gather (random 64-byte row gather of known size, for PMC
+                                      calibration of gathers)
        python bench.py --mode fwd|bwd --config c2|c5 (one entry only, for rocprofv3)
        python bench.py --mode fused --config c2|c5 (producer-fused op against the modules'
                                                     order of operations)
@@ -138,16 +145,29 @@ class GpuCase:
         return self.core.backward(self.dim, self.grad_out, self.value, self.levels, self.loc,
                                   self.attn, True, 1e-4)
 
-    def step(self):
+    def step(self, shapes=None):
         import msda_triton
 
         op = msda_triton.msda2d if self.dim == 2 else msda_triton.msda3d
         v = self.value.detach().requires_grad_(True)
         lo = self.loc.detach().requires_grad_(True)
         a = self.attn.detach().requires_grad_(True)
-        out = op(v, self.shapes, lo, a, True, 1e-4)
+        out = op(v, self.shapes if shapes is None else shapes, lo, a, True, 1e-4)
         out.backward(self.grad_out)
         return out
+
+    def step_cloning(self):
+        """fwd+bwd the way the reference benchmark times it (benchmark_msda2d.py:210-218):
+        inputs cloned and grad_output drawn with randn_like inside the timed region."""
+        import msda_triton
+
+        op = msda_triton.msda2d if self.dim == 2 else msda_triton.msda3d
+        v = self.value.clone().detach().requires_grad_(True)
+        lo = self.loc.clone().detach().requires_grad_(True)
+        a = self.attn.clone().detach().requires_grad_(True)
+        out = op(v, self.shapes, lo, a, True, 1e-4)
+        out.backward(torch.randn_like(out))
+        return v.grad, lo.grad, a.grad
 
 
 def time_events(fn, iters, warmup):
@@ -165,7 +185,28 @@ def time_events(fn, iters, warmup):
     return e0.elapsed_time(e1) / iters
 
 
-def measure_case(cfg, device, steps, warmup):
+FLUSH_BYTES = 512 << 20  # larger than MI355X's 256 MB MALL
+
+
+def time_flushed(fn, iters, warmup, flush):
+    """Median ms per call of fn with the caches flushed before each call: `flush` (a buffer
+    larger than the MALL) is rewritten between calls, outside each call's event pair."""
+    for _ in range(warmup):
+        fn()
+    evs = []
+    for i in range(iters):
+        flush.fill_(i & 0xFF)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        evs.append((e0, e1))
+    torch.cuda.synchronize()
+    return statistics.median(a.elapsed_time(b) for a, b in evs)
+
+
+def measure_case(cfg, device, steps, warmup, flush=None):
     case = GpuCase(cfg, device)
     byt = algorithmic_bytes(cfg)
     fwd_ms = time_events(case.fwd, max(steps, 20), warmup)
@@ -185,7 +226,7 @@ def measure_case(cfg, device, steps, warmup):
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
     step_ms = max(e0.elapsed_time(e1) / steps, wall_ms)
     gbps = lambda b, ms: b / (ms * 1e-3) / 1e9  # noqa: E731
-    return {
+    res = {
         "config": cfg,
         "bytes": byt,
         "fwd_ms": fwd_ms,
@@ -195,6 +236,12 @@ def measure_case(cfg, device, steps, warmup):
         "bwd_gbps": gbps(byt["bwd"], bwd_ms),
         "step_gbps": gbps(byt["fwd_bwd"], step_ms),
     }
+    if flush is not None:
+        n = max(steps, 20)
+        res["fwd_ms_flushed"] = time_flushed(case.fwd, n, warmup, flush)
+        res["step_ms_flushed"] = time_flushed(case.step, n, warmup, flush)
+        res["step_ms_cloning"] = time_events(case.step_cloning, max(steps, 10), warmup)
+    return res
 
 
 def measure_fused(cfg, device, steps, warmup):
@@ -254,6 +301,18 @@ def measure_fused(cfg, device, steps, warmup):
                     "value, reference points, offsets and logits"}
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (from /proc/cpuinfo), else the platform's description."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
 def cpu_baseline(cfg, q_sample=None, reps=3):
     """The oracle (torch grid_sample restatement, fp32 on upcast inputs) timed on the host
     CPU: fwd + backward of out.sum(), on the first q_sample queries of the workload."""
@@ -283,11 +342,12 @@ def cpu_baseline(cfg, q_sample=None, reps=3):
         "value": round(byt / t / 1e9, 4),
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
+        "cpu_model": cpu_model(),
         "kind": "port",
         "sample": (f"oracle/torch_ref.msda_ref fwd+bwd(out.sum()) in fp32 on bf16-rounded inputs, "
                    f"first {q_sample} of {cfg['Q']} queries, median of {reps}; "
                    f"{t * 1e3:.1f} ms per sample, {t * 1e3 * cfg['Q'] / q_sample:.0f} ms "
-                   f"per full step by linear scaling; CPU {platform.processor() or platform.machine()}"),
+                   f"per full step by linear scaling; CPU {cpu_model()}"),
     }
 
 
@@ -308,7 +368,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--mode", choices=["full", "fwd", "bwd", "step", "copy", "fused"], default="full")
+    ap.add_argument("--mode", choices=["full", "fwd", "bwd", "step", "copy", "gather", "fused"],
+                    default="full")
     ap.add_argument("--config", choices=sorted(CONFIGS), default="c2")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-queries", type=int, default=None)
@@ -332,6 +393,17 @@ def main():
         ms = time_events(lambda: dst.copy_(src), args.steps, args.warmup)
         print(json.dumps({"mode": "copy", "bytes_read": n, "bytes_written": n, "ms": ms}))
         return
+    if args.mode == "gather":
+        # 16 M random 64-byte rows (bf16, 32 channels) out of a 4 GiB table, far beyond the
+        # MALL: each row is fetched from HBM once; int32 indices, output written once
+        rows, n = (4 << 30) // 64, 1 << 24
+        table = torch.empty(rows, 32, dtype=torch.bfloat16, device=device).fill_(1.0)
+        idx = torch.randperm(rows, device=device)[:n].to(torch.int32)
+        out = torch.empty(n, 32, dtype=torch.bfloat16, device=device)
+        ms = time_events(lambda: torch.index_select(table, 0, idx, out=out), args.steps, args.warmup)
+        print(json.dumps({"mode": "gather", "bytes_read": n * 64 + n * 4, "bytes_written": n * 64,
+                          "rows": n, "ms": ms}))
+        return
     if args.mode == "fused":
         r = measure_fused(CONFIGS[args.config], device, args.steps, args.warmup)
         print(json.dumps({"mode": "fused", "config": args.config, **r}))
@@ -344,8 +416,14 @@ def main():
         return
 
     main_cfg, also_cfg = CONFIGS["c2"], CONFIGS["c5"]
-    r = measure_case(main_cfg, device, args.steps, args.warmup)
-    r5 = measure_case(also_cfg, device, args.steps, args.warmup)
+    flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device=device)
+    r = measure_case(main_cfg, device, args.steps, args.warmup, flush)
+    r5 = measure_case(also_cfg, device, args.steps, args.warmup, flush)
+    # C2 with the level shapes resident on the GPU (the backward plans on the device)
+    c2 = GpuCase(main_cfg, device)
+    shapes_dev = c2.shapes.to(device, torch.int32)
+    c2_gpu_shapes_ms = time_events(lambda: c2.step(shapes_dev), max(args.steps, 20), args.warmup)
+    del flush
     # the other BASELINE.json configurations: C2 in fp32, C4 (3D 2-level) in fp32 and bf16,
     # and C3 (decoder cross-attention, forward only: host and launch latency bound)
     extra = {}
@@ -376,12 +454,16 @@ def main():
         cpu = cpu_baseline(main_cfg, q_sample=args.cpu_queries)
 
     def summary(x):
-        return {"fwd_ms": round(x["fwd_ms"], 5), "fwd_bwd_ms": round(x["step_ms"], 5),
-                "bwd_ms": round(x["bwd_ms"], 5), "bwd_gbps": round(x["bwd_gbps"], 2),
-                "fwd_gbps": round(x["fwd_gbps"], 2),
-                "fwd_roofline_frac": round(x["fwd_gbps"] / HBM_PEAK_GBPS, 4),
-                "fwd_bwd_gbps": round(x["step_gbps"], 2),
-                "bytes_fwd": x["bytes"]["fwd"], "bytes_fwd_bwd": x["bytes"]["fwd_bwd"]}
+        out = {"fwd_ms": round(x["fwd_ms"], 5), "fwd_bwd_ms": round(x["step_ms"], 5),
+               "bwd_ms": round(x["bwd_ms"], 5), "bwd_gbps": round(x["bwd_gbps"], 2),
+               "fwd_gbps": round(x["fwd_gbps"], 2),
+               "fwd_roofline_frac": round(x["fwd_gbps"] / HBM_PEAK_GBPS, 4),
+               "fwd_bwd_gbps": round(x["step_gbps"], 2),
+               "bytes_fwd": x["bytes"]["fwd"], "bytes_fwd_bwd": x["bytes"]["fwd_bwd"]}
+        for k in ("fwd_ms_flushed", "step_ms_flushed", "step_ms_cloning"):
+            if k in x:
+                out[k.replace("step_", "fwd_bwd_")] = round(x[k], 5)
+        return out
 
     line = {
         "metric": METRIC,
@@ -400,7 +482,7 @@ def main():
                                "(BASELINE.json configs[1])",
                    "B": 2, "H": 8, "C": 32, "levels": main_cfg["shapes"], "K": num_keys(main_cfg),
                    "Q": main_cfg["Q"], "P": 4, "clamp_grid": True, "clamp_eps": 1e-4},
-        "c2_bf16": summary(r),
+        "c2_bf16": dict(summary(r), fwd_bwd_ms_gpu_shapes=round(c2_gpu_shapes_ms, 5)),
         "also": {"c5_bf16_3d_4level": summary(r5),
                  **{k: summary(v) for k, v in extra.items()},
                  "c3_bf16_decoder": {"fwd_ms": round(c3_fwd_ms, 5),

@@ -7,6 +7,7 @@
 // enqueue everything on the caller's stream. No allocation, no synchronisation, no global
 // mutable state except the thread-local error text.
 #include <math.h>
+#include <mutex>
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -38,7 +39,6 @@ const char* dtype_name(int dt) {
 }
 
 constexpr uint64_t kLim31 = 0x7FFFFFFFull;
-constexpr uint64_t kCus = 256;  // MI355X compute units: workgroups of the staged forward
 constexpr uint32_t kChunkRecords = 4096;        // records per tile-kernel chunk (rounded to S)
 // LDS share of one tile workgroup at the kernel's occupancy target (160 KB LDS per CU):
 // four workgroups in 2D, two in 3D
@@ -46,7 +46,39 @@ constexpr uint32_t kTileLdsTarget2 = 40 * 1024 - 256;
 constexpr uint32_t kTileLdsTarget3 = 80 * 1024 - 256;
 constexpr uint32_t kTileLdsBudget = 160 * 1024 - 256;  // one workgroup per CU
 constexpr int kMaxBinsLds = 8192;  // bin histogram + bases in 64 KB of LDS
-constexpr uint64_t kL2Bytes = 4ull << 20;  // L2 of one XCD
+
+// The current device's compute units, XCDs and per-XCD L2 bytes, which size the staged
+// forward's grid, the head-major rule and the XCD-contiguous workgroup mappings. Read once
+// per device (hipDeviceGetAttribute); a whole MI355X (256 CUs, 8 XCDs of 4 MB L2) where no
+// device answers, e.g. for the host-only workspace queries on a machine without a GPU.
+struct Machine {
+  uint32_t cus;
+  uint32_t xcds;
+  uint64_t l2_bytes;  // L2 of one XCD
+};
+
+Machine machine() {
+  static std::mutex mu;
+  static Machine cache[64];
+  static bool have[64];
+  Machine m{256u, 8u, 4ull << 20};
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return m;
+  std::lock_guard<std::mutex> lock(mu);
+  if (have[dev]) return cache[dev];
+  int cus = 0, l2 = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0) {
+    m.cus = (uint32_t)cus;
+    m.xcds = (uint32_t)cus / msda::kCusPerXcd;
+    if (m.xcds < 1) m.xcds = 1;
+  }
+  // the attribute is one XCD's L2 on MI3xx; a figure above 8 MB would be the sum over XCDs
+  if (hipDeviceGetAttribute(&l2, hipDeviceAttributeL2CacheSize, dev) == hipSuccess && l2 > 0)
+    m.l2_bytes = (uint64_t)l2 > (8ull << 20) ? (uint64_t)l2 / m.xcds : (uint64_t)l2;
+  cache[dev] = m;
+  have[dev] = true;
+  return m;
+}
 
 // Lanes per unit and per-lane vector width for one C-channel value row.
 struct Layout {
@@ -152,7 +184,7 @@ int64_t batches_per_launch(const msda_desc* d, const Layout& lay) {
 bool use_head_major(const msda_desc* d) {
   const uint64_t row = (uint64_t)d->channels * elem_bytes(d->value_dtype);
   const uint64_t gathers = (uint64_t)d->num_queries * d->num_levels * d->num_points << d->dim;
-  return d->num_heads > 1 && row <= 64 && (uint64_t)d->num_keys * 128 > kL2Bytes &&
+  return d->num_heads > 1 && row <= 64 && (uint64_t)d->num_keys * 128 > machine().l2_bytes &&
          gathers >= 8 * (uint64_t)d->num_keys;
 }
 
@@ -176,6 +208,7 @@ void fill_params(const msda_desc* d, const Layout& lay, int64_t nb, msda::Params
   p->hi_g = (float)(1.0 - d->clamp_eps);
   const uint64_t lanes = (uint64_t)p->num_units << lay.lpu_log2;
   p->nblocks = (uint32_t)((lanes + msda::kBlock - 1) / msda::kBlock);
+  p->xcds = machine().xcds;
   p->value_bytes = (uint32_t)(nb * (uint64_t)d->num_keys * H * d->channels * elem_bytes(d->value_dtype));
 }
 
@@ -350,7 +383,7 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
     const uint64_t upw2 = 2u * (uint64_t)pl.upw;
     const uint64_t wgs2 = (uint64_t)(((uint64_t)d->batch * d->num_heads) >> hg) *
                           ((((uint64_t)d->num_queries << hg) + upw2 - 1) / upw2);
-    if (wgs2 >= (uint64_t)msda::kGradWgsPerCu * kCus) pl.upw = (int32_t)upw2;
+    if (wgs2 >= (uint64_t)msda::kGradWgsPerCu * machine().cus) pl.upw = (int32_t)upw2;
   }
   pl.wgpg = (int32_t)((((uint64_t)d->num_queries << hg) + pl.upw - 1) / pl.upw);
   pl.R = (kChunkRecords + pl.S - 1) / pl.S * pl.S;
@@ -371,7 +404,8 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
   const uint64_t samples =
       (uint64_t)nb * d->num_queries * d->num_heads * d->num_levels * d->num_points;
   pl.max_chunks = atomic ? 0u : pl.T_cap + (uint32_t)((samples + pl.R - 1) / pl.R);
-  pl.grid_chunks = (pl.max_chunks + msda::kXcds - 1) / msda::kXcds * msda::kXcds;
+  pl.xcds = machine().xcds;
+  pl.grid_chunks = (pl.max_chunks + pl.xcds - 1) / pl.xcds * pl.xcds;
   pl.value_bytes = (uint32_t)(nb * (uint64_t)d->num_keys * d->num_heads * d->channels * s);
   pl.grad_loc_elems = samples * (uint64_t)d->dim;
   out->sz = msda::bwd_sizes(pl, samples, d->dim);
@@ -472,7 +506,8 @@ int fwd_impl(const msda_desc* d, const void* value, const int32_t* spatial_shape
     // Staged kernel: one workgroup per CU, each (batch, head) slice split into query
     // ranges; used when every workgroup gets enough queries to amortise its LDS copy.
     const uint64_t slices = (uint64_t)bc * d->num_heads;
-    const uint64_t splits = (kCus + slices - 1) / slices;
+    const uint64_t cus = machine().cus;
+    const uint64_t splits = (cus + slices - 1) / slices;
     const uint64_t qper = ((uint64_t)d->num_queries + splits - 1) / splits;
     // the LDS holds at least one staged row beside the all-zero row
     const bool staged = has_samples && qper >= msda::kFwdStageMinQueries &&

@@ -289,7 +289,7 @@ __global__ __launch_bounds__(kGradThreads) void bwd_grad_kernel(const BwdPlan pl
   const int bins = geo->bins;
   const bool mul24 = geo->mul24 != 0;
   // workgroups of one (batch, head-group) are contiguous and dealt to one XCD
-  const uint32_t lb = xcd_logical_block(blockIdx.x, gridDim.x);
+  const uint32_t lb = xcd_logical_block(blockIdx.x, gridDim.x, pl.xcds);
   const uint32_t g = lb / (uint32_t)pl.wgpg;
   const uint32_t w = lb - g * (uint32_t)pl.wgpg;
   if constexpr (!AT) {
@@ -567,7 +567,7 @@ __global__ __launch_bounds__(kBlock) void bwd_fill_kernel(const BwdPlan pl, cons
   // 2D: a group's workgroups in a contiguous range per XCD, so its record lines are
   // written through one L2 (C2 fill 48 -> 44 us); 3D keeps them dealt round-robin
   // (C5 105 against 110 us grouped)
-  const uint32_t lbk = DIM == 2 ? xcd_logical_block(blockIdx.x, gridDim.x) : blockIdx.x;
+  const uint32_t lbk = DIM == 2 ? xcd_logical_block(blockIdx.x, gridDim.x, pl.xcds) : blockIdx.x;
   const uint32_t g = lbk / (uint32_t)pl.wgpg;
   const uint32_t w = lbk - g * (uint32_t)pl.wgpg;
   for (int i = threadIdx.x; i < bins; i += kBlock)
@@ -751,15 +751,16 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
   typedef typename EV::T TV;
   extern __shared__ __attribute__((aligned(16))) char s_mem[];
 
-  // Chunks are dealt to XCDs in contiguous ranges (workgroup i runs on XCD i % 8), so the
+  // Chunks are dealt to XCDs in contiguous ranges (workgroup i runs on XCD i % xcds), so the
   // chunks of one (batch, head-group) share an XCD and its L2.
   const GeoP geo = geo_of(bf);
   if (geo->atomic) return;
   const uint32_t total = bf.chunk_off[geo->T];
-  const uint32_t per = (total + kXcds - 1) / kXcds;
-  const uint32_t slot = blockIdx.x / kXcds;
+  const uint32_t xcds = pl.xcds;
+  const uint32_t per = (total + xcds - 1) / xcds;
+  const uint32_t slot = blockIdx.x / xcds;
   if (slot >= per) return;
-  const uint32_t c = (blockIdx.x % kXcds) * per + slot;
+  const uint32_t c = (blockIdx.x % xcds) * per + slot;
   if (c >= total) return;  // the whole workgroup exits
   const uint32_t t = bf.chunk_tile[c];
   const uint32_t off = bf.chunk_off[t];
@@ -978,7 +979,7 @@ __global__ __launch_bounds__(kBlock) void bwd_fold_kernel(const BwdPlan pl, cons
   const GeoP geo = geo_of(bf);
   const uint32_t T = geo->T;
   if (geo->atomic || blockIdx.x >= T) return;
-  const uint32_t t = xcd_logical_block(blockIdx.x, T);
+  const uint32_t t = xcd_logical_block(blockIdx.x, T, pl.xcds);
   const uint32_t off = bf.chunk_off[t];
   const uint32_t nch = bf.chunk_off[t + 1] - off;
   BwdLevel lv;

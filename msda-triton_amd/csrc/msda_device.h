@@ -12,7 +12,7 @@ namespace msda {
 
 constexpr int kBlock = 256;            // threads per workgroup (4 waves)
 constexpr int kWave = 64;
-constexpr int kXcds = 8;               // MI355X: 8 XCDs, workgroups dealt round-robin
+constexpr int kCusPerXcd = 32;         // gfx950 (MI350 / MI355): 32 compute units per XCD
 constexpr uint32_t kOobOffset = 0x80000000u;  // buffer offset that always fails the range check
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -251,15 +251,16 @@ __device__ inline float group_sum(float v, int lg) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Workgroup index with XCD-contiguous ownership: the hardware deals workgroups to the 8
-// XCDs round-robin, so physical block i runs on XCD i % 8. Remap so XCD x owns one
-// contiguous range of logical blocks; consecutive logical blocks cover consecutive
-// (batch, head-group) slices, which then stay resident in that XCD's L2.
-__device__ inline uint32_t xcd_logical_block(uint32_t bid, uint32_t nblocks) {
-  uint32_t xcd = bid % kXcds;
-  uint32_t idx = bid / kXcds;
-  uint32_t per = nblocks / kXcds;
-  uint32_t rem = nblocks % kXcds;
+// Workgroup index with XCD-contiguous ownership: the hardware deals workgroups to the
+// device's `xcds` XCDs round-robin (8 on a whole MI355X, fewer in a partition), so
+// physical block i runs on XCD i % xcds. Remap so XCD x owns one contiguous range of
+// logical blocks; consecutive logical blocks cover consecutive (batch, head-group) slices,
+// which then stay resident in that XCD's L2.
+__device__ inline uint32_t xcd_logical_block(uint32_t bid, uint32_t nblocks, uint32_t xcds) {
+  uint32_t xcd = bid % xcds;
+  uint32_t idx = bid / xcds;
+  uint32_t per = nblocks / xcds;
+  uint32_t rem = nblocks % xcds;
   return xcd * per + (xcd < rem ? xcd : rem) + idx;
 }
 

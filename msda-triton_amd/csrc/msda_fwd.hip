@@ -32,7 +32,7 @@ struct Unit {
 };
 
 __device__ inline bool decode_unit(const Params& p, Unit& u) {
-  const uint32_t lb = xcd_logical_block(blockIdx.x, p.nblocks);
+  const uint32_t lb = xcd_logical_block(blockIdx.x, p.nblocks, p.xcds);
   const uint32_t t = lb * kBlock + threadIdx.x;
   const uint32_t unit = t >> p.lpu_log2;
   u.lane = t & ((1u << p.lpu_log2) - 1u);
@@ -575,7 +575,7 @@ __global__ __launch_bounds__(kFwdStageThreads) void msda_fwd_staged_kernel(const
   __syncthreads();
   const uint32_t zrow = s_pfx[s_nst] / nvec * lrs;  // byte offset of the all-zero row
 
-  const uint32_t lb = xcd_logical_block(blockIdx.x, p.nblocks);
+  const uint32_t lb = xcd_logical_block(blockIdx.x, p.nblocks, p.xcds);
   const uint32_t bh = lb / p.splits, split = lb - bh * p.splits;
   const uint32_t b = bh / (uint32_t)p.H, h = bh - b * (uint32_t)p.H;
   const uint32_t q0 = split * p.qper;

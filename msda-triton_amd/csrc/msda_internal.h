@@ -59,6 +59,7 @@ struct Params {
   int32_t clamp;
   float lo_g, hi_g;        // grid clamp bounds as fp32
   uint32_t nblocks;
+  uint32_t xcds;           // XCDs of the device (workgroups are dealt to them round-robin)
   int32_t coords_aligned;  // loc and attn are 16-byte aligned: per-level block loads allowed
   // staged path: one workgroup per (batch, head, query range) keeps the smallest levels of
   // its (batch, head) value slice in LDS
@@ -241,7 +242,8 @@ struct BwdPlan {
   uint32_t lds_g_bytes;        // bytes of the staged fp32 grad_out rows of a sub-batch
   uint32_t lds_bytes;          // total dynamic LDS of the tile kernel
   uint32_t max_chunks;         // upper bound of the chunk count
-  uint32_t grid_chunks;        // tile-kernel grid: max_chunks rounded up to 8 (one per XCD)
+  uint32_t grid_chunks;        // tile-kernel grid: max_chunks rounded up to a multiple of xcds
+  uint32_t xcds;               // XCDs of the device (workgroups are dealt to them round-robin)
   uint64_t grad_loc_elems;     // Bc * Q * H * L * P * dim (NaN fill of invalid shapes)
 };
 
