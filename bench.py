@@ -352,15 +352,17 @@ def cpu_baseline(cfg, q_sample=None, reps=3):
 
 
 def load_traffic(key: str):
-    """HBM bytes per launch (FETCH_SIZE and WRITE_SIZE, copy-calibrated) from the committed
-    rocprofv3 --pmc summary profiles/traffic.json, if present."""
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary profiles/traffic.json:
+    (FETCH_SIZE scaled by the streaming-copy factor + WRITE_SIZE, the same with the
+    random-row gather factor), or (None, None)."""
     f = REPO / "profiles" / "traffic.json"
-    if not f.exists():
-        return None
     try:
-        return json.loads(f.read_text()).get(key)
+        e = json.loads(f.read_text()).get(key)
     except (OSError, ValueError):
-        return None
+        return None, None
+    if isinstance(e, dict):
+        return e.get("copy_calibrated"), e.get("gather_calibrated")
+    return e, None
 
 
 def main():
@@ -441,9 +443,10 @@ def main():
     # scans, tile and fold kernels on the same stream) is reported beside it as a group
     def roof(kname, kbytes, kms, key):
         achieved = kbytes / (kms * 1e-3) / 1e9
+        traffic, traffic_g = load_traffic(key)
         return {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                "traffic": load_traffic(key), "kernel": kname,
+                "traffic": traffic, "traffic_gather_calibrated": traffic_g, "kernel": kname,
                 "algorithmic_bytes_per_launch": kbytes, "avg_launch_ms": round(kms, 5)}
 
     roofline = roof(FWD_KERNEL, r["bytes"]["fwd"], r["fwd_ms"], "msda_fwd:c2_bf16")
