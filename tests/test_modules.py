@@ -3,23 +3,27 @@
 CPU: init_weights patterns against what their geometry fixes (2D: the eight compass
 directions scaled to the unit square, times p + 1; 3D: points on circles of radius
 0.5 * 0.02 * (p + 1) in (x, y) with z = 2 * radius * sin(2 * angle)), argument checks, and
-that the module refuses CPU tensors (no CPU fallback).
-GPU: forward and parameter gradients equal those of the same module whose sampling step
-is the oracle (oracle/torch_ref), run on the CPU in fp32, within 1e-4 normwise; exercised
-with query and head chunking, padding mask, positional encoding, sequence-first layout and
-checkpointing, for the fused (locations and softmax in the kernel) and unfused paths.
+that the module refuses CPU tensors (no CPU fallback). The module oracle
+(oracle/module_ref.msda_module_ref, the reference modules' forward restated) is pinned by
+a closed form: identity projections, uniform softmax and integer pixel offsets from
+pixel-centre reference points on non-square levels sample exact value rows, so the output
+is the identity plus the mean of known rows.
+GPU: forward and parameter gradients of MSDA2D / MSDA3D (HIP op, fp32) equal those of the
+module oracle evaluated in float64 on the CPU from the same parameters, within 1e-4
+normwise; exercised with query and head chunking, padding mask, positional encoding,
+sequence-first layout and checkpointing, for the fused (locations and softmax in the
+kernel) and unfused paths.
 """
 
 from __future__ import annotations
 
-import copy
 import math
 
 import pytest
 import torch
 
 from msda_triton.pytorch import MSDA2D, MSDA3D
-from oracle import torch_ref
+from oracle import module_ref
 from tests._util import max_rel
 
 
@@ -82,13 +86,69 @@ def test_cpu_tensors_are_refused():
           reference_points=torch.rand(1, 5, 1, 2), spatial_shapes=torch.tensor([[2, 3]]))
 
 
-def _oracle_module(m):
-    """A CPU copy of module m whose sampling step is the oracle."""
-    r = copy.deepcopy(m).cpu()
-    r._msda = lambda v, s, lo, a: torch_ref.msda_ref(v, s, lo, a, r.clamp_grid, r.clamp_eps)
-    r._msda_fused = lambda v, s, rf, o, lg: torch_ref.msda_fused_ref(v, s, rf, o, lg, r.clamp_grid,
-                                                                     r.clamp_eps)
-    return r
+def _params(m, dtype=torch.float64):
+    return {k: v.detach().cpu().to(dtype) for k, v in m.state_dict().items()}
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+def test_module_oracle_closed_form(dim):
+    """Identity value/output projections, zero attention logits (uniform weights over L*P)
+    and offsets of whole pixels from pixel-centre reference points: every sample lands on a
+    pixel centre and returns that value row exactly, on non-square levels, so the output is
+    identity + the mean over (l, p) of known rows. A swapped x/y pixel offset gives
+    different rows (the case distinguishes the normaliser's axis order)."""
+    E, H, L, P, bs, nq = 8, 2, 2, 3, 2, 5
+    C = E // H
+    # every extent >= 3: a reference pixel one inside the border plus a shift of at most
+    # one pixel stays inside the level
+    shapes = torch.tensor([[5, 7], [3, 4]] if dim == 2 else [[3, 4, 5], [3, 3, 4]])
+    sizes = shapes.prod(-1).tolist()
+    starts = [0, sizes[0]]
+    nv = sum(sizes)
+    g = torch.Generator().manual_seed(0)
+    eye = torch.eye(E, dtype=torch.float64)
+    # whole-pixel offsets per (h, l, p, axis): small, so reference + offset stays inside
+    shift = torch.randint(-1, 2, (H, L, P, dim), generator=g)
+    params = {"value_proj.weight": eye, "value_proj.bias": torch.zeros(E, dtype=torch.float64),
+              "output_proj.weight": eye, "output_proj.bias": torch.zeros(E, dtype=torch.float64),
+              "attention_weights.weight": torch.zeros(H * L * P, E, dtype=torch.float64),
+              "attention_weights.bias": torch.zeros(H * L * P, dtype=torch.float64),
+              "sampling_offsets.weight": torch.zeros(H * L * P * dim, E, dtype=torch.float64),
+              "sampling_offsets.bias": shift.reshape(-1).to(torch.float64)}
+    query = torch.randn(nq, bs, E, generator=g, dtype=torch.float64)   # sequence-first
+    value = torch.randn(nv, bs, E, generator=g, dtype=torch.float64)
+    # reference pixel (x, y[, z]) per (b, q, l), one pixel inside the level's border
+    ext = shapes.flip(-1)  # (W, H[, D]) per level
+    pix = torch.stack([torch.randint(1, int(e) - 1, (bs, nq), generator=g) for e in ext.reshape(-1)], -1)
+    pix = pix.view(bs, nq, L, dim)
+    refp = (pix.to(torch.float64) + 0.5) / ext.to(torch.float64)
+    out = module_ref.msda_module_ref(dim, params, query, value=value, reference_points=refp,
+                                     spatial_shapes=shapes, num_heads=H, num_levels=L,
+                                     num_points=P)
+
+    def expected(sh):
+        want = query.clone()
+        for b in range(bs):
+            for q in range(nq):
+                for h in range(H):
+                    acc = torch.zeros(C, dtype=torch.float64)
+                    for lv in range(L):
+                        W_, H_ = int(ext[lv, 0]), int(ext[lv, 1])
+                        for p in range(P):
+                            x, y = (pix[b, q, lv, :2] + sh[h, lv, p, :2]).tolist()
+                            k = starts[lv] + y * W_ + x
+                            if dim == 3:
+                                z = int(pix[b, q, lv, 2] + sh[h, lv, p, 2])
+                                k = starts[lv] + (z * H_ + y) * W_ + x
+                            acc += value[k, b, h * C:(h + 1) * C]
+                    want[q, b, h * C:(h + 1) * C] += acc / (L * P)
+        return want
+
+    assert (out - expected(shift)).abs().max().item() < 1e-10
+    swapped = shift.clone()
+    swapped[..., [0, 1]] = shift[..., [1, 0]]
+    if not torch.equal(swapped, shift):
+        assert (out - expected(swapped)).abs().max().item() > 1e-3
 
 
 @pytest.mark.gpu
@@ -101,21 +161,21 @@ def test_module_matches_oracle_module(dim, fused):
     cls = MSDA2D if dim == 2 else MSDA3D
     shapes = torch.tensor([[12, 10], [6, 5]] if dim == 2 else [[4, 6, 5], [2, 3, 3]])
     nv = int(shapes.prod(-1).sum())
-    E, H, nq, bs = 64, 4, 37, 2
-    m = cls(E, num_heads=H, num_levels=2, num_points=3, dropout=0.0, query_chunk_size=16,
+    E, H, L, P, nq, bs = 64, 4, 2, 3, 37, 2
+    m = cls(E, num_heads=H, num_levels=L, num_points=P, dropout=0.0, query_chunk_size=16,
             head_chunk_size=3, use_checkpoint=True, fused=fused)
     m.init_weights()
     with torch.no_grad():  # non-trivial offsets and weights
         m.sampling_offsets.weight.normal_(0, 0.05)
         m.attention_weights.weight.normal_(0, 0.2)
     m.train()
-    ref = _oracle_module(m)
+    params = {k: v.requires_grad_(True) for k, v in _params(m).items()}
     print(f"module parity dim={dim} fused={fused}", flush=True)
     g = torch.Generator().manual_seed(1)
     query = torch.randn(nq, bs, E, generator=g)          # sequence-first (batch_first=False)
     value = torch.randn(nv, bs, E, generator=g)
     pos = torch.randn(nq, bs, E, generator=g)
-    refp = torch.rand(bs, nq, 2, dim, generator=g)
+    refp = torch.rand(bs, nq, L, dim, generator=g)
     mask = torch.rand(bs, nv, generator=g) < 0.1
     grad = torch.randn(nq, bs, E, generator=g)
     dev = torch.device("cuda")
@@ -123,10 +183,15 @@ def test_module_matches_oracle_module(dim, fused):
     out = m(query.to(dev), value=value.to(dev), query_pos=pos.to(dev), key_padding_mask=mask.to(dev),
             reference_points=refp.to(dev), spatial_shapes=shapes)
     out.backward(grad.to(dev))
-    out_r = ref(query, value=value, query_pos=pos, key_padding_mask=mask, reference_points=refp,
-                spatial_shapes=shapes)
-    out_r.backward(grad)
+    d = torch.float64
+    out_r = module_ref.msda_module_ref(dim, params, query.to(d), value=value.to(d),
+                                       query_pos=pos.to(d), key_padding_mask=mask,
+                                       reference_points=refp.to(d), spatial_shapes=shapes,
+                                       num_heads=H, num_levels=L, num_points=P)
+    out_r.backward(grad.to(d))
     assert out.shape == (nq, bs, E)
     assert max_rel(out.detach().cpu(), out_r.detach()) <= 1e-4
-    for (name, p), (_, pr) in zip(m.named_parameters(), ref.named_parameters()):
-        assert max_rel(p.grad.cpu(), pr.grad) <= 1e-4, name
+    for name, p in m.named_parameters():
+        assert p.grad is not None, name
+        err = max_rel(p.grad.cpu(), params[name].grad)
+        assert err <= 1e-4, (name, err)
