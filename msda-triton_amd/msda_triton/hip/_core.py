@@ -31,9 +31,19 @@ _LEVEL_CACHE_MAX = 64
 # that tensor is alive and unmodified (same version counter): a loop over one shapes
 # tensor pays the device-side conversion once.
 _GPU_LEVEL_CACHE: OrderedDict = OrderedDict()
-# The same identity cache for CPU-resident shape tensors (entries also hold K): a loop over
-# one shapes tensor skips reading it back into Python on every call.
+# The same identity cache for CPU-resident shape tensors (entries also hold K and the
+# tensor's raw bytes, compared on every hit, since writes through a numpy view of the
+# tensor do not bump its version counter): a loop over one shapes tensor skips converting
+# it in Python on every call.
 _CPU_ID_CACHE: OrderedDict = OrderedDict()
+
+
+def _raw_bytes(t: torch.Tensor):
+    """The raw bytes of a small CPU tensor (None if it has no plain numpy view)."""
+    try:
+        return t.detach().numpy().tobytes()
+    except (RuntimeError, TypeError):
+        return None
 
 
 def validate_inputs(name: str, dim: int, value: torch.Tensor, value_spatial_shapes: torch.Tensor,
@@ -107,10 +117,11 @@ def prepare_levels(dim: int, value: torch.Tensor, value_spatial_shapes: torch.Te
     if value_spatial_shapes.device.type == "cpu":
         key = id(value_spatial_shapes)
         hit = _CPU_ID_CACHE.get(key)
+        raw = _raw_bytes(value_spatial_shapes)
         if hit is not None:
-            ref, version, hdim, hdev, total_keys, levels = hit
+            ref, version, hdim, hdev, total_keys, levels, hraw = hit
             if (ref() is value_spatial_shapes and version == value_spatial_shapes._version
-                    and hdim == dim and hdev == device):
+                    and hdim == dim and hdev == device and raw is not None and raw == hraw):
                 _check_num_keys(dim, value, total_keys)
                 _CPU_ID_CACHE.move_to_end(key)
                 return levels
@@ -120,7 +131,8 @@ def prepare_levels(dim: int, value: torch.Tensor, value_spatial_shapes: torch.Te
             ref = weakref.ref(value_spatial_shapes)
         except TypeError:
             return levels
-        _CPU_ID_CACHE[key] = (ref, value_spatial_shapes._version, dim, device, total_keys, levels)
+        _CPU_ID_CACHE[key] = (ref, value_spatial_shapes._version, dim, device, total_keys, levels,
+                              raw)
         if len(_CPU_ID_CACHE) > _LEVEL_CACHE_MAX:
             _CPU_ID_CACHE.popitem(last=False)
         return levels

@@ -210,6 +210,24 @@ def test_prepare_levels_cpu_shape_checks():
     assert lv.host.tolist() == [[3, 3], [2, 2]]
 
 
+def test_cpu_shapes_cache_follows_writes_through_numpy_views():
+    """The identity cache of CPU shape tensors compares the tensor's bytes on every hit: a
+    write through a numpy view (which does not bump the version counter) is seen, even when
+    K is unchanged (H and W swapped)."""
+    from msda_triton.hip import _core
+
+    shapes = torch.tensor([[3, 4], [2, 2]])
+    value = torch.zeros(1, 16, 1, 4)
+    a = _core.prepare_levels(2, value, shapes)
+    assert a.host.tolist() == [[3, 4], [2, 2]]
+    assert _core.prepare_levels(2, value, shapes) is a  # identity hit
+    shapes.numpy()[0] = [4, 3]
+    v0 = shapes._version
+    b = _core.prepare_levels(2, value, shapes)
+    assert shapes._version == v0  # the write did not bump the version
+    assert b.host.tolist() == [[4, 3], [2, 2]]
+
+
 def test_public_api_surface():
     """Same export sites and names as the reference (src/msda_triton/__init__.py:16-27,
     triton/__init__.py:10-22, pytorch/__init__.py:10-20)."""
