@@ -329,6 +329,13 @@ __global__ __launch_bounds__(kGradThreads) void bwd_grad_kernel(const BwdPlan pl
         load_block<EC, SB * DIM>(cb, locp);
         load_block<EC, SB>(ab, attp);
       }
+      // lane j of the group keeps the gradients of batch j of every group of `lanes`
+      // consecutive batches; the lanes store them together, so a wave writes whole lines
+      float hga[SB], hgl[SB * DIM];
+#pragma unroll
+      for (int k = 0; k < SB; ++k) hga[k] = 0.0f;
+#pragma unroll
+      for (int k = 0; k < SB * DIM; ++k) hgl[k] = 0.0f;
 #pragma unroll 1
       for (int bi = 0; bi < nbatch; ++bi) {
         const BwdLevel lv = level_at(geo, bi / BPL);
@@ -365,10 +372,20 @@ __global__ __launch_bounds__(kGradThreads) void bwd_grad_kernel(const BwdPlan pl
           if constexpr (!AT)
             if (any[k] && lane == ((uint32_t)k & (lanes - 1u))) atomicAdd(&s_hist[bin[k]], 1u);
         }
-        // the batch's gradients are contiguous per unit: one block store each
-        if (lane == 0) {
-          store_block<EC, SB>(gap + bi * SB, ga);
-          store_block<EC, SB * DIM>(glp + bi * (SB * DIM), gl);
+        const uint32_t slot = (uint32_t)bi & (lanes - 1u);
+        if (slot == lane) {
+#pragma unroll
+          for (int k = 0; k < SB; ++k) hga[k] = ga[k];
+#pragma unroll
+          for (int k = 0; k < SB * DIM; ++k) hgl[k] = gl[k];
+        }
+        if (slot == lanes - 1u || bi + 1 == nbatch) {
+          // batches bi - slot .. bi: lane j stores batch bi - slot + j, all contiguous
+          const int mine = bi - (int)slot + (int)lane;
+          if (mine <= bi) {
+            store_block<EC, SB>(gap + mine * SB, hga);
+            store_block<EC, SB * DIM>(glp + mine * (SB * DIM), hgl);
+          }
         }
       }
     } else {
