@@ -62,13 +62,18 @@ __device__ inline BwdLevel level_at(GeoP g, int l) {
 }
 
 // ------------------------------------------------------------------ block scans
+// Inclusive scan across the 64 lanes of a wave with DPP: Hillis-Steele within each row of
+// 16 lanes (row_shr 1, 2, 4, 8; lanes shifted in from outside the row read 0), then lane 15's
+// sum added to rows 1 and 3 (row_bcast:15) and lane 31's to rows 2 and 3 (row_bcast:31).
+// No LDS round trip (the ds_bpermute ladder it replaces cost six). Every lane of the wave
+// must be active.
 __device__ inline uint32_t wave_incl_scan(uint32_t v) {
-  const int lane = threadIdx.x & (kWave - 1);
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const uint32_t t = __shfl_up(v, d, kWave);
-    if (lane >= d) v += t;
-  }
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, true);   // row_shr:1
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, true);   // row_shr:2
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, true);   // row_shr:4
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, true);   // row_shr:8
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false);  // row_bcast:31
   return v;
 }
 
@@ -127,12 +132,28 @@ __device__ inline TileCoord decode_tile(const BwdPlan& pl, GeoP geo, uint32_t t,
   return tc;
 }
 
-// Region-cell index of a corner relative to the tile origin, or -1 outside the region.
-__device__ inline int region_cell(const BwdPlan& pl, int ox, int oy, int oz) {
-  if ((unsigned)ox >= (unsigned)pl.RX || (unsigned)oy >= (unsigned)pl.RY ||
-      (unsigned)oz >= (unsigned)pl.RZ)
+// The cells of a tile's region (the tile plus a one-cell high-side halo) that lie inside
+// the level, numbered x fastest: a tile on the level's high edge has no halo there, and a
+// partial tile only its own columns and rows. Corners never fall outside the level, so
+// every cell of this compact region can receive entries.
+struct Region {
+  int ex, ey, ez;
+};
+
+__device__ inline Region tile_region(const BwdPlan& pl, const TileCoord& tc, const BwdLevel& lv) {
+  Region rg;
+  rg.ex = min(pl.RX, lv.W - tc.X0);
+  rg.ey = min(pl.RY, lv.H - tc.Y0);
+  rg.ez = min(pl.RZ, lv.D - tc.Z0);
+  return rg;
+}
+
+// Compact region-cell index of a corner relative to the tile origin, or -1 outside.
+__device__ inline int region_cell(const Region& rg, int ox, int oy, int oz) {
+  if ((unsigned)ox >= (unsigned)rg.ex || (unsigned)oy >= (unsigned)rg.ey ||
+      (unsigned)oz >= (unsigned)rg.ez)
     return -1;
-  return (oz * pl.RY + oy) * pl.RX + ox;
+  return (oz * rg.ey + oy) * rg.ex + ox;
 }
 
 // Unit of a bin workgroup: the wi-th of the upw units of workgroup w of group g.
@@ -521,7 +542,7 @@ __global__ __launch_bounds__(kBlock) void bwd_colscan_kernel(const BwdPlan pl, c
       const int i = base + u * kWave + (int)lane;
       const uint32_t inc = wave_incl_scan(v[u]);
       if (i < pl.wgpg) c[i] = run + inc - v[u];
-      run += __shfl(inc, kWave - 1, kWave);
+      run += (uint32_t)__builtin_amdgcn_readlane((int)inc, kWave - 1);
     }
   }
   if (lane == 0) bf.bin_start[t] = run;
@@ -703,8 +724,8 @@ __device__ inline Sample<DIM> record_sample(const uint32_t* rec, const BwdLevel&
 }
 
 template <int DIM>
-__device__ inline int corner_cell(const BwdPlan& pl, const TileCoord& tc, const Sample<DIM>& sm, int cc) {
-  return region_cell(pl, sm.ax.i0 + (cc & 1) - tc.X0, sm.ay.i0 + ((cc >> 1) & 1) - tc.Y0,
+__device__ inline int corner_cell(const Region& rg, const TileCoord& tc, const Sample<DIM>& sm, int cc) {
+  return region_cell(rg, sm.ax.i0 + (cc & 1) - tc.X0, sm.ay.i0 + ((cc >> 1) & 1) - tc.Y0,
                      DIM == 3 ? sm.az.i0 + ((cc >> 2) & 1) - tc.Z0 : 0);
 }
 
@@ -724,22 +745,34 @@ __device__ inline void lds_f32(const char* p, float (&v)[N]) {
   }
 }
 
-// Exclusive scan, in place, of the n + 1 counters of a region by one wave; c[n] gets the
-// total. Every lane of the wave must call it.
+// Exclusive scan, in place, of the n + 1 counters c[0..n] of a region by one wave (c[n] is
+// zero before, the total after). c is 16-byte aligned and padded to a multiple of four
+// counters; each lane scans a run of whole quads (one 16-byte read and write each; a
+// region of up to 255 cells is one quad per lane). Every lane of the wave must call it.
 __device__ inline void wave_scan_counts(uint32_t* c, int n) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int per = (n + kWave - 1) / kWave;
-  const int i0 = lane * per, i1 = min(n, i0 + per);
-  uint32_t sum = 0;
-  for (int i = i0; i < i1; ++i) sum += c[i];
-  const uint32_t inc = wave_incl_scan(sum);
-  uint32_t run = inc - sum;
-  for (int i = i0; i < i1; ++i) {
-    const uint32_t v = c[i];
-    c[i] = run;
-    run += v;
+  const int nq = (n + 4) >> 2;
+  uint4* q = reinterpret_cast<uint4*>(c);
+  if (nq <= kWave) {
+    const uint4 v = lane < nq ? q[lane] : make_uint4(0u, 0u, 0u, 0u);
+    const uint32_t sum = v.x + v.y + v.z + v.w;
+    const uint32_t run = wave_incl_scan(sum) - sum;
+    if (lane < nq) q[lane] = make_uint4(run, run + v.x, run + v.x + v.y, run + v.x + v.y + v.z);
+    return;
   }
-  if (lane == kWave - 1) c[n] = inc;
+  const int per = (nq + kWave - 1) / kWave;
+  const int i0 = lane * per, i1 = min(nq, i0 + per);
+  uint32_t sum = 0;
+  for (int i = i0; i < i1; ++i) {
+    const uint4 v = q[i];
+    sum += v.x + v.y + v.z + v.w;
+  }
+  uint32_t run = wave_incl_scan(sum) - sum;
+  for (int i = i0; i < i1; ++i) {
+    const uint4 v = q[i];
+    q[i] = make_uint4(run, run + v.x, run + v.x + v.y, run + v.x + v.y + v.z);
+    run += v.x + v.y + v.z + v.w;
+  }
 }
 
 // One workgroup (kTileThreads<DIM> threads) per chunk of a tile's records, in sub-batches of
@@ -769,16 +802,27 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
   extern __shared__ __attribute__((aligned(16))) char s_mem[];
 
   // Chunks are dealt to XCDs in contiguous ranges (workgroup i runs on XCD i % xcds), so the
-  // chunks of one (batch, head-group) share an XCD and its L2.
+  // chunks of one (batch, head-group) share an XCD and its L2. When the groups divide evenly
+  // over the XCDs, each XCD takes whole groups, whose chunks run coarsest level first: the
+  // longest chunks start first. (Equal-size ranges split groups, and a group cut at the end
+  // of one XCD's range left its coarse chunks to start last: C5 tile 487 -> 435 us.)
   const GeoP geo = geo_of(bf);
   if (geo->atomic) return;
-  const uint32_t total = bf.chunk_off[geo->T];
   const uint32_t xcds = pl.xcds;
-  const uint32_t per = (total + xcds - 1) / xcds;
-  const uint32_t slot = blockIdx.x / xcds;
-  if (slot >= per) return;
-  const uint32_t c = (blockIdx.x % xcds) * per + slot;
-  if (c >= total) return;  // the whole workgroup exits
+  const uint32_t slot = blockIdx.x / xcds, x = blockIdx.x % xcds;
+  uint32_t c;
+  if ((uint32_t)pl.groups % xcds == 0u) {
+    const uint32_t tiles_x = (uint32_t)pl.groups / xcds * (uint32_t)geo->bins;
+    const uint32_t c0 = bf.chunk_off[x * tiles_x], c1 = bf.chunk_off[(x + 1) * tiles_x];
+    c = c0 + slot;
+    if (c >= c1) return;  // the whole workgroup exits
+  } else {
+    const uint32_t total = bf.chunk_off[geo->T];
+    const uint32_t per = (total + xcds - 1) / xcds;
+    if (slot >= per) return;
+    c = x * per + slot;
+    if (c >= total) return;
+  }
   const uint32_t t = bf.chunk_tile[c];
   const uint32_t off = bf.chunk_off[t];
   const uint32_t nch = bf.chunk_off[t + 1] - off;
@@ -791,8 +835,14 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
   const uint32_t grow = (uint32_t)pl.C * 4u;  // bytes of one staged fp32 grad_out row
   char* s_g = s_mem;                                                   // [S][C] fp32
   uint2* s_ent = reinterpret_cast<uint2*>(s_g + pl.lds_g_bytes);       // [S * NC]
-  uint32_t* s_cnt2 = reinterpret_cast<uint32_t*>(s_ent + (size_t)S * NC);  // 2 x [rcells + 1]
-  const int ncell_r = pl.rcells;
+  // two counter sets of rcells + 1 counters, each padded to whole quads (16-byte aligned:
+  // S * C * 4 and S * NC * 8 are multiples of 16)
+  uint32_t* s_cnt2 = reinterpret_cast<uint32_t*>(s_ent + (size_t)S * NC);
+  // compact region: the owner items and counters cover only its cells (a partial tile on a
+  // coarse level's edge spreads its entries over all owner threads instead of the few whose
+  // fixed-layout cells it touches: C2 level-3 edge chunks 176 -> 110 us, tile kernel 174 -> 161 us)
+  const Region rg = tile_region(pl, tc, lv);
+  const int ncell_r = rg.ex * rg.ey * rg.ez;
   const uint32_t nvec = (uint32_t)pl.nvec;
   const int tid = (int)threadIdx.x;
   const int lane = tid & (kWave - 1), wv = tid >> 6;
@@ -806,7 +856,8 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
 #pragma unroll
     for (int k = 0; k < OV; ++k) acc[m][k] = 0.0f;
 
-  for (int i = tid; i < 2 * (ncell_r + 1); i += NT) s_cnt2[i] = 0u;
+  const int ncp = (pl.rcells + 4) & ~3;  // counter-set stride, sized for a full region
+  for (int i = tid; i < 2 * ncp; i += NT) s_cnt2[i] = 0u;
   uint32_t rec[RW];
 #pragma unroll
   for (int k = 0; k < RW; ++k) rec[k] = 0u;
@@ -819,7 +870,7 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
   int par = 0;
   for (uint32_t sb = beg; sb < end; sb += S, par ^= 1) {
     const uint32_t nrec = min(S, end - sb);
-    uint32_t* s_cnt = s_cnt2 + par * (ncell_r + 1);
+    uint32_t* s_cnt = s_cnt2 + par * ncp;
     const bool has = (uint32_t)tid < nrec;
 
     // 1. grad_out rows -> LDS as fp32; corner ranks
@@ -849,7 +900,7 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
         sm = record_sample<DIM>(rec, lv);
 #pragma unroll
         for (int cc = 0; cc < NC; ++cc) {
-          const int ce = corner_cell<DIM>(pl, tc, sm, cc);
+          const int ce = corner_cell<DIM>(rg, tc, sm, cc);
           slot[cc] = 0xffffffffu;
           if (corner_valid<DIM>(cc, sm) && ce >= 0)
             slot[cc] = ((uint32_t)ce << 16) | atomicAdd(&s_cnt[ce], 1u);
@@ -876,7 +927,7 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
     // 2. scan this set of counters; clear the other (last read in the previous sub-batch)
     if (wv == 0) wave_scan_counts(s_cnt, ncell_r);
     {
-      uint32_t* o = s_cnt2 + (par ^ 1) * (ncell_r + 1);
+      uint32_t* o = s_cnt2 + (par ^ 1) * ncp;
       for (int i = tid; i <= ncell_r; i += NT) o[i] = 0u;
     }
     lds_sync();
@@ -901,35 +952,58 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
     }
     lds_sync();
 
-    // 4. owner pass: fp32 register accumulation per (region cell, channel chunk)
+    // 4. owner pass: fp32 register accumulation per (region cell, channel chunk). Every
+    // item's entry range is read first (one LDS round trip for all of them); within an item,
+    // four entries per step (their entry and row reads are independent, so their LDS
+    // latencies overlap) and a tail of up to three entries in one step (entries past the end
+    // re-read the first one with weight zero). Reading the next step's entries during a step
+    // was slower: the register copies cost more issue than the round trip they hide.
+    uint32_t eb[MI], ee[MI];
 #pragma unroll
     for (int m = 0; m < MI; ++m) {
       const int it = tid + m * NT;
+      eb[m] = ee[m] = 0u;
       if (it < ncell_r * onv) {
-        const int ce = (int)fdiv((uint32_t)it, pl.div_onv), ch = it - ce * onv;
-        const uint32_t e0 = s_cnt[ce], e1 = s_cnt[ce + 1];
-        const char* gb = s_g + ch * (OV * 4);
-        // four entries per step: their entry and row reads are independent, so their LDS
-        // latencies overlap
-        uint32_t e = e0;
-        for (; e + 4 <= e1; e += 4) {
-          uint2 en[4];
+        const int ce = (int)fdiv((uint32_t)it, pl.div_onv);
+        eb[m] = s_cnt[ce];
+        ee[m] = s_cnt[ce + 1];
+      }
+    }
 #pragma unroll
-          for (int j = 0; j < 4; ++j) en[j] = s_ent[e + j];
-          float gv[4][OV];
+    for (int m = 0; m < MI; ++m) {
+      const int it = tid + m * NT;
+      if (it >= ncell_r * onv) continue;
+      const int ce = (int)fdiv((uint32_t)it, pl.div_onv), ch = it - ce * onv;
+      const char* gb = s_g + ch * (OV * 4);
+      uint32_t e = eb[m];
+      const uint32_t e1 = ee[m];
+      for (; e + 4 <= e1; e += 4) {
+        uint2 en[4];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) lds_f32<OV>(gb + en[j].y, gv[j]);
+        for (int j = 0; j < 4; ++j) en[j] = s_ent[e + j];
+        float gv[4][OV];
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 4; ++j) lds_f32<OV>(gb + en[j].y, gv[j]);
 #pragma unroll
-            for (int k = 0; k < OV; ++k) acc[m][k] = __builtin_fmaf(as_float(en[j].x), gv[j][k], acc[m][k]);
-        }
-        for (; e < e1; ++e) {
-          const uint2 en = s_ent[e];
-          float gv[OV];
-          lds_f32<OV>(gb + en.y, gv);
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-          for (int k = 0; k < OV; ++k) acc[m][k] = __builtin_fmaf(as_float(en.x), gv[k], acc[m][k]);
+          for (int k = 0; k < OV; ++k) acc[m][k] = __builtin_fmaf(as_float(en[j].x), gv[j][k], acc[m][k]);
+      }
+      if (e < e1) {
+        const uint32_t r = e1 - e;  // 1 .. 3
+        const uint2 t0 = s_ent[e];
+        const uint2 t1 = s_ent[r > 1 ? e + 1 : e];
+        const uint2 t2 = s_ent[r > 2 ? e + 2 : e];
+        float g0[OV], g1[OV], g2[OV];
+        lds_f32<OV>(gb + t0.y, g0);
+        lds_f32<OV>(gb + t1.y, g1);
+        lds_f32<OV>(gb + t2.y, g2);
+        const float w1 = r > 1 ? as_float(t1.x) : 0.0f, w2 = r > 2 ? as_float(t2.x) : 0.0f;
+#pragma unroll
+        for (int k = 0; k < OV; ++k) {
+          acc[m][k] = __builtin_fmaf(as_float(t0.x), g0[k], acc[m][k]);
+          acc[m][k] = __builtin_fmaf(w1, g1[k], acc[m][k]);
+          acc[m][k] = __builtin_fmaf(w2, g2[k], acc[m][k]);
         }
       }
     }
@@ -944,10 +1018,10 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
     const int it = (int)threadIdx.x + m * NT;
     if (it >= ncell_r * onv) continue;
     const int cell = (int)fdiv((uint32_t)it, pl.div_onv), ch = it - cell * onv;
-    const int rz = (int)fdiv((uint32_t)cell, pl.div_rxy), rxy = cell - rz * pl.RX * pl.RY;
-    const int ry = (int)fdiv((uint32_t)rxy, pl.div_rx), rx = rxy - ry * pl.RX;
+    const int exy = rg.ex * rg.ey;  // compact region extents: once per chunk, plain division
+    const int rz = cell / exy, rxy = cell - rz * exy;
+    const int ry = rxy / rg.ex, rx = rxy - ry * rg.ex;
     const int x = tc.X0 + rx, y = tc.Y0 + ry, z = tc.Z0 + rz;
-    if (x >= lv.W || y >= lv.H || z >= lv.D) continue;
     const bool owned = rx < pl.TX && ry < pl.TY && rz < pl.TZ;
     const bool interior = owned && rx > 0 && ry > 0 && (DIM == 2 || rz > 0);
     if (nch == 1 && interior) {
@@ -956,7 +1030,9 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
                             (((size_t)tc.b * pl.K + row) * pl.H + tc.h) * pl.C + ch * OV,
                         acc[m]);
     } else {
-      float* dst = bf.scratch + ((size_t)c * ncell_r + cell) * pl.C + ch * OV;
+      // partials in the fold's full-region layout
+      const int full = (rz * pl.RY + ry) * pl.RX + rx;
+      float* dst = bf.scratch + ((size_t)c * pl.rcells + full) * pl.C + ch * OV;
       store_vec<F32, OV>(dst, acc[m]);
     }
   }

@@ -212,7 +212,6 @@ struct BwdPlan {
   FastDiv div_nvec;            // divisor nvec (value-load chunks per row)
   int32_t onv;                 // owner chunks per row in the tile kernel: C / tile_owner_vec(VEC)
   FastDiv div_onv;             // divisor onv (owner item -> cell, chunk)
-  FastDiv div_rx, div_rxy;     // divisors RX and RX * RY (region cell -> rx, ry, rz)
   FastDiv div_tx, div_txy;     // divisors TX and TX * TY (owned cell -> lx, ly, lz)
   int32_t RX, RY, RZ;          // region: tile + 1 along each axis (RZ = 1 in 2D)
   int32_t cells;               // owned cells per tile: TX * TY * TZ
