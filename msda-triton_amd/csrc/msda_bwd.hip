@@ -1062,10 +1062,15 @@ __device__ inline void add_partials(float (&o)[VEC], const float* src, size_t st
 
 // One workgroup per tile. Sums, for every edge cell (and every cell of a split tile), the
 // partials of the tile's own chunks and then the halo partials of the chunks of the lower
-// neighbours whose halo covers the cell, and writes the cell in the value dtype.
+// neighbours whose halo covers the cell, and writes the cell in the value dtype. The
+// neighbours' chunk ranges are the same for the whole tile and are read once. When the tile
+// and its neighbours are one chunk each (the common case), a cell's partial loads are all
+// issued before the first addition, in one round trip instead of one per source (C5 fold
+// 88 -> 75 us, C2 15 -> 14 us); the additions keep the same order either way.
 template <int DIM, typename EV, int VEC>
 __global__ __launch_bounds__(kBlock) void bwd_fold_kernel(const BwdPlan pl, const BwdBuffers bf) {
   typedef typename EV::T TV;
+  constexpr int NB = 1 << DIM;  // source 0: the tile's own chunks; nb > 0: neighbour at -(dx, dy, dz)
   // tiles in contiguous ranges per XCD, like the tile kernel's chunks, so most partials
   // are read from the L2 that wrote them (the grid may exceed the launch's tiles when it was
   // sized without the shapes; the extra workgroups exit)
@@ -1073,11 +1078,27 @@ __global__ __launch_bounds__(kBlock) void bwd_fold_kernel(const BwdPlan pl, cons
   const uint32_t T = geo->T;
   if (geo->atomic || blockIdx.x >= T) return;
   const uint32_t t = xcd_logical_block(blockIdx.x, T, pl.xcds);
-  const uint32_t off = bf.chunk_off[t];
-  const uint32_t nch = bf.chunk_off[t + 1] - off;
   BwdLevel lv;
   const TileCoord tc = decode_tile(pl, geo, t, &lv);
   const uint32_t bins = (uint32_t)geo->bins;
+  uint32_t soff[NB], scnt[NB];
+  soff[0] = bf.chunk_off[t];
+  scnt[0] = bf.chunk_off[t + 1] - soff[0];
+  bool single = scnt[0] == 1u;
+#pragma unroll
+  for (int nb = 1; nb < NB; ++nb) {
+    const int dx = nb & 1, dy = (nb >> 1) & 1, dz = (nb >> 2) & 1;
+    soff[nb] = 0u;
+    scnt[nb] = 0u;
+    if ((dx && tc.tx == 0) || (dy && tc.ty == 0) || (dz && tc.tz == 0)) continue;
+    const int tibn = lv.tile_off + ((tc.tz - dz) * lv.nty + (tc.ty - dy)) * lv.ntx + (tc.tx - dx);
+    const uint32_t tn = tc.g * bins + (((uint32_t)tibn << pl.hg_log2) | tc.hsub);
+    soff[nb] = bf.chunk_off[tn];
+    scnt[nb] = bf.chunk_off[tn + 1] - soff[nb];
+    single = single && scnt[nb] == 1u;
+  }
+  const uint32_t nch = scnt[0];
+  const size_t stride = (size_t)pl.rcells * pl.C;  // floats between chunks' partials
   TV* gv = static_cast<TV*>(bf.grad_value);
   for (int i = threadIdx.x; i < pl.cells * pl.nvec; i += kBlock) {
     const int cell = (int)fdiv((uint32_t)i, pl.div_nvec), ch = i - cell * pl.nvec;
@@ -1087,23 +1108,37 @@ __global__ __launch_bounds__(kBlock) void bwd_fold_kernel(const BwdPlan pl, cons
     if (x >= lv.W || y >= lv.H || z >= lv.D) continue;
     const bool interior = lx > 0 && ly > 0 && (DIM == 2 || lz > 0);
     if (nch == 1 && interior) continue;  // written by the tile kernel
+    // each source's first partial of this cell (its region cell in that tile's layout)
+    const float* src[NB];
+    bool use[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const int dx = nb & 1, dy = (nb >> 1) & 1, dz = (nb >> 2) & 1;
+      use[nb] = scnt[nb] > 0u && (!dx || lx == 0) && (!dy || ly == 0) && (!dz || lz == 0);
+      const int rn = ((lz + dz * pl.TZ) * pl.RY + (ly + dy * pl.TY)) * pl.RX + (lx + dx * pl.TX);
+      src[nb] = bf.scratch + ((size_t)soff[nb] * pl.rcells + rn) * pl.C + ch * VEC;
+    }
     float o[VEC];
 #pragma unroll
     for (int k = 0; k < VEC; ++k) o[k] = 0.0f;
-    const int rc = (lz * pl.RY + ly) * pl.RX + lx;
-    add_partials<VEC>(o, bf.scratch + ((size_t)off * pl.rcells + rc) * pl.C + ch * VEC,
-                      (size_t)pl.rcells * pl.C, nch);
-    for (int nb = 1; nb < (1 << DIM); ++nb) {
-      const int dx = nb & 1, dy = (nb >> 1) & 1, dz = (nb >> 2) & 1;
-      if ((dx && (lx != 0 || tc.tx == 0)) || (dy && (ly != 0 || tc.ty == 0)) ||
-          (dz && (lz != 0 || tc.tz == 0)))
-        continue;
-      const int tibn = lv.tile_off + ((tc.tz - dz) * lv.nty + (tc.ty - dy)) * lv.ntx + (tc.tx - dx);
-      const uint32_t tn = tc.g * bins + (((uint32_t)tibn << pl.hg_log2) | tc.hsub);
-      const int rn = ((lz + dz * pl.TZ) * pl.RY + (ly + dy * pl.TY)) * pl.RX + (lx + dx * pl.TX);
-      const uint32_t noff = bf.chunk_off[tn], nn = bf.chunk_off[tn + 1] - noff;
-      add_partials<VEC>(o, bf.scratch + ((size_t)noff * pl.rcells + rn) * pl.C + ch * VEC,
-                        (size_t)pl.rcells * pl.C, nn);
+    if (single) {
+      float v[NB][VEC];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+        if (use[nb]) {
+#pragma unroll
+          for (int k = 0; k < VEC; ++k) v[nb][k] = src[nb][k];
+        }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+        if (use[nb]) {
+#pragma unroll
+          for (int k = 0; k < VEC; ++k) o[k] += v[nb][k];
+        }
+    } else {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+        if (use[nb]) add_partials<VEC>(o, src[nb], stride, scnt[nb]);
     }
     const uint32_t row = (uint32_t)lv.start + ((uint32_t)z * lv.H + y) * lv.W + x;
     store_vec<EV, VEC>(gv + (((size_t)tc.b * pl.K + row) * pl.H + tc.h) * pl.C + ch * VEC, o);
