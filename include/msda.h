@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define MSDA_ABI_VERSION 4
+#define MSDA_ABI_VERSION 5
 
 typedef enum msda_dtype {
   MSDA_F32 = 0,
@@ -65,9 +65,21 @@ typedef struct msda_desc {
   int32_t coord_dtype;  /* msda_dtype of sampling_locations, attention_weights and their
                            gradients; must equal value_dtype or be MSDA_F32 */
   int32_t clamp_grid;   /* nonzero: clamp the [-1, 1] sampling grid to [-1+eps, 1-eps] */
-  int32_t reserved;     /* must be 0 */
+  int32_t flags;        /* MSDA_FLAG_* bits; 0 for none */
   double clamp_eps;     /* eps of the clamp above (reference default 1e-4) */
 } msda_desc;
+
+/*
+ * msda_desc.flags bit, for the backward entry points only (msda_bwd, msda_bwd_dev,
+ * msda_bwd_fused, msda_bwd_fused_dev, msda_bwd_noalloc; the forward entry points and their
+ * workspace queries reject it): `value` points to a head-major (B, H, K, C) copy of the
+ * value tensor instead of the (B, K, H, C) tensor itself, such as the copy msda_fwd leaves
+ * at the start of its workspace when msda_fwd_workspace_bytes() equals the whole value's
+ * bytes. The backward then gathers from it directly and makes no copy of its own (the 3D
+ * 4-level training step saves one 25 us relayout and 77 MB of workspace). The caller keeps
+ * the copy alive and unchanged until the backward has run. No counterpart in the reference.
+ */
+#define MSDA_FLAG_VALUE_HEAD_MAJOR 1
 
 /* ABI version of the loaded library (MSDA_ABI_VERSION it was built with). */
 int msda_abi_version(void);

@@ -133,7 +133,8 @@ int validate(const msda_desc* d) {
                 "sampling_locations/attention_weights dtype %s must equal value dtype %s or be "
                 "float32",
                 dtype_name(d->coord_dtype), dtype_name(d->value_dtype));
-  if (d->reserved != 0) return fail(MSDA_ERR_INVALID, "reserved field must be 0");
+  if (d->flags & ~MSDA_FLAG_VALUE_HEAD_MAJOR)
+    return fail(MSDA_ERR_INVALID, "unknown flags 0x%x", (unsigned)d->flags);
   if (!isfinite(d->clamp_eps)) return fail(MSDA_ERR_INVALID, "clamp_eps must be finite");
   if (d->num_keys > (int64_t)kLim31)
     return fail(MSDA_ERR_INVALID, "number of keys (%lld) exceeds int32 range",
@@ -357,7 +358,9 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
   pl.static_atomic = atomic ? 1 : 0;
   pl.fallback = dev && !atomic ? 1 : 0;
   if (atomic) tiles = 0;
-  const bool head_major = !atomic && use_head_major(d);
+  // value already head-major (MSDA_FLAG_VALUE_HEAD_MAJOR): gather from it, copy nothing
+  const bool hm_given = (d->flags & MSDA_FLAG_VALUE_HEAD_MAJOR) != 0;
+  const bool head_major = hm_given || (!atomic && use_head_major(d));
   // Heads whose rows share 128-byte lines are grouped (their units and chunks run on one
   // XCD). A head-major copy shares no lines across heads: one head per group then keeps
   // one head's value and grad_out rows per XCD (C5: tile 699 -> 523 us, sample gradients
@@ -375,6 +378,7 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
   pl.div_lp = msda::make_fastdiv((uint32_t)(d->num_levels * d->num_points > 0
                                                 ? d->num_levels * d->num_points : 1));
   pl.head_major = head_major ? 1 : 0;
+  pl.hm_given = hm_given ? 1 : 0;
   pl.hg_log2 = hg;
   pl.bins_cap = (int32_t)bins_cap;
   pl.upw = (msda::kGradThreads >> lay.lpu_log2) * msda::kGradRounds;
@@ -435,6 +439,8 @@ void carve(char* ws, const msda::BwdSizes& z, msda::BwdBuffers* bf) {
   p += al(z.geom_bytes);
   bf->counts = reinterpret_cast<uint32_t*>(p);
   p += al(z.counts * 4);
+  bf->tile_n = reinterpret_cast<uint32_t*>(p);
+  p += al(z.tile_n * 4);
   bf->bin_start = reinterpret_cast<uint32_t*>(p);
   p += al(z.bin_start * 4);
   bf->chunk_off = reinterpret_cast<uint32_t*>(p);
@@ -457,6 +463,7 @@ int fwd_impl(const msda_desc* d, const void* value, const int32_t* spatial_shape
              const int32_t* level_start, const void* sampling_locations,
              const void* attention_weights, const float* ref, void* output, void* workspace,
              size_t workspace_bytes, void* stream, bool fused) {
+  if (d && d->flags) return fail(MSDA_ERR_INVALID, "forward: flags apply to the backward only");
   const char* name = fused ? "msda_fwd_fused" : "msda_fwd";
   int rc = validate(d);
   if (rc) return rc;
@@ -662,7 +669,9 @@ int bwd_impl(const msda_desc* d, const int32_t* hs, const int32_t* ds, const voi
     bf.grad_attn = static_cast<char*>(grad_attention_weights) + (uint64_t)b0 * qh * LP * sc;
     pl.coords_aligned = aligned(bf.loc, 16) && aligned(bf.attn, 16) && aligned(bf.grad_loc, 16) &&
                         aligned(bf.grad_attn, 16);
-    if (pl.head_major) {
+    if (pl.hm_given) {
+      bf.value_h = bf.value;  // this launch's batches of the caller's head-major copy
+    } else if (pl.head_major) {
       hipError_t e = msda::launch_head_major(bf.value, const_cast<void*>(bf.value_h), (uint32_t)bc,
                                              (uint32_t)d->num_keys, (uint32_t)d->num_heads,
                                              (uint32_t)(d->channels * sv), hp.lay.vec_bytes, st);
@@ -762,6 +771,7 @@ int msda_validate(const msda_desc* desc) {
 size_t msda_fwd_workspace_bytes(const msda_desc* d) {
   g_err[0] = 0;
   if (validate(d)) return 0;
+  if (d->flags) return fail(MSDA_ERR_INVALID, "msda_fwd_workspace_bytes: flags apply to the backward only"), 0;
   if (!use_head_major(d) || d->batch == 0 || d->num_queries == 0) return 0;
   Layout lay;
   const void* none[1] = {nullptr};

@@ -492,18 +492,28 @@ __global__ __launch_bounds__(kBlock) void bwd_clear_sums_kernel(const BwdPlan pl
 // Atomic path: round the fp32 sums to the value dtype, VEC elements per thread and step
 // (n is a multiple of VEC: C is). Invalid device shapes: every gradient becomes NaN
 // (n_loc grad_loc elements and n_attn = n_loc / DIM grad_attn elements in the coord dtype).
+// The sums follow the layout the sample-gradient kernel gathered from: (Bc, H, K, C) for
+// head-major plans, whose element (b, k, h, c) of grad_value is read across that transpose.
 template <typename EV, typename EC, int VEC>
-__global__ __launch_bounds__(kBlock) void bwd_round_kernel(const BwdBuffers bf, uint32_t n,
-                                                           uint64_t n_loc, int dim) {
+__global__ __launch_bounds__(kBlock) void bwd_round_kernel(const BwdPlan pl, const BwdBuffers bf,
+                                                           uint32_t n, uint64_t n_loc, int dim) {
   const GeoP geo = geo_of(bf);
   if (!geo->atomic) return;
   const bool nan = geo->invalid != 0;
   const uint32_t stride = gridDim.x * (uint32_t)kBlock * VEC;
   typename EV::T* dst = static_cast<typename EV::T*>(bf.grad_value);
+  const uint32_t C = (uint32_t)pl.C, H = (uint32_t)pl.H, K = (uint32_t)pl.K;
   for (uint32_t i = (blockIdx.x * (uint32_t)kBlock + threadIdx.x) * VEC; i < n; i += stride) {
+    uint32_t src = i;
+    if (pl.head_major) {
+      const uint32_t row = i / C, c = i - row * C;  // row = (b * K + k) * H + h
+      const uint32_t bk = row / H, h = row - bk * H;
+      const uint32_t b = bk / K, k = bk - b * K;
+      src = ((b * H + h) * K + k) * C + c;
+    }
     float v[VEC];
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) v[e] = nan ? __builtin_nanf("") : bf.sums[i + e];
+    for (int e = 0; e < VEC; ++e) v[e] = nan ? __builtin_nanf("") : bf.sums[src + e];
     store_vec<EV, VEC>(dst + i, v);
   }
   if (nan) {
@@ -520,7 +530,7 @@ __global__ __launch_bounds__(kBlock) void bwd_round_kernel(const BwdBuffers bf, 
 
 // ------------------------------------------------------------------ 2: column scan
 // One wave per tile: the tile's counts over the bin workgroups of its group become
-// offsets within the tile, and its total goes to bin_start[t].
+// offsets within the tile, and its total goes to tile_n[t].
 __global__ __launch_bounds__(kBlock) void bwd_colscan_kernel(const BwdPlan pl, const BwdBuffers bf) {
   const GeoP geo = geo_of(bf);
   const uint32_t t = blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
@@ -545,41 +555,77 @@ __global__ __launch_bounds__(kBlock) void bwd_colscan_kernel(const BwdPlan pl, c
       run += (uint32_t)__builtin_amdgcn_readlane((int)inc, kWave - 1);
     }
   }
-  if (lane == 0) bf.bin_start[t] = run;
+  if (lane == 0) bf.tile_n[t] = run;
 }
 
 // ------------------------------------------------------------------ 3: plan
-// One workgroup. Each thread owns a contiguous range of tiles: scans record totals into
-// first-record offsets, cuts each tile into max(1, ceil(n / R)) chunks (an empty tile
-// still gets one chunk, which writes its zeros), and fills the chunk -> tile table.
+// One workgroup per (batch, head-group): the record totals of the group's tiles become
+// first-record offsets, each tile is cut into max(1, ceil(n / R)) chunks (an empty tile
+// still gets one chunk, which writes its zeros), and the chunk -> tile table is filled.
+// Each workgroup first sums the totals of the tiles of all earlier groups (coalesced loads
+// and a workgroup reduction), then scans its own tiles, each thread a contiguous range.
+// (One workgroup for all tiles spent 14 us of C5's backward on the stores of one CU.)
 __global__ __launch_bounds__(kPlanThreads) void bwd_plan_kernel(const BwdPlan pl, const BwdBuffers bf) {
   __shared__ uint32_t s_w[kPlanThreads / kWave];
   const GeoP geo = geo_of(bf);
   if (geo->atomic) return;
-  const uint32_t T = geo->T;
-  const uint32_t per = (T + kPlanThreads - 1) / kPlanThreads;
-  const uint32_t t0 = min(T, threadIdx.x * per), t1 = min(T, t0 + per);
+  const uint32_t T = geo->T, bins = (uint32_t)geo->bins;
+  const uint32_t ta = blockIdx.x * bins, tb = ta + bins;
+  auto chunks = [&](uint32_t n) { return max(1u, (n + pl.R - 1) / pl.R); };
+  uint32_t bn = 0, bc = 0;  // records and chunks of the earlier groups
+  {
+    uint32_t sn = 0, sc = 0;
+#pragma unroll 8
+    for (uint32_t t = threadIdx.x; t < ta; t += kPlanThreads) {
+      const uint32_t n = bf.tile_n[t];
+      sn += n;
+      sc += chunks(n);
+    }
+    block_excl_scan<kPlanThreads>(sn, s_w, &bn);
+    block_excl_scan<kPlanThreads>(sc, s_w, &bc);
+  }
+  const uint32_t per = (bins + kPlanThreads - 1) / kPlanThreads;
+  const uint32_t t0 = min(tb, ta + threadIdx.x * per), t1 = min(tb, t0 + per);
+  // up to PB tiles per thread: their totals are loaded together and kept in registers
+  constexpr uint32_t PB = 16;
+  uint32_t nv[PB];
   uint32_t sn = 0, sc = 0;
-  for (uint32_t t = t0; t < t1; ++t) {
-    const uint32_t n = bf.bin_start[t];
-    sn += n;
-    sc += max(1u, (n + pl.R - 1) / pl.R);
+  if (per <= PB) {
+#pragma unroll
+    for (uint32_t k = 0; k < PB; ++k) nv[k] = t0 + k < t1 ? bf.tile_n[t0 + k] : 0u;
+#pragma unroll
+    for (uint32_t k = 0; k < PB; ++k) {
+      sn += nv[k];
+      if (t0 + k < t1) sc += chunks(nv[k]);
+    }
+  } else {
+    for (uint32_t t = t0; t < t1; ++t) {
+      const uint32_t n = bf.tile_n[t];
+      sn += n;
+      sc += chunks(n);
+    }
   }
   uint32_t tot_n, tot_c;
-  uint32_t pn = block_excl_scan<kPlanThreads>(sn, s_w, &tot_n);
-  uint32_t pc = block_excl_scan<kPlanThreads>(sc, s_w, &tot_c);
-  for (uint32_t t = t0; t < t1; ++t) {
-    const uint32_t n = bf.bin_start[t];
-    const uint32_t nch = max(1u, (n + pl.R - 1) / pl.R);
+  uint32_t pn = bn + block_excl_scan<kPlanThreads>(sn, s_w, &tot_n);
+  uint32_t pc = bc + block_excl_scan<kPlanThreads>(sc, s_w, &tot_c);
+  auto place = [&](uint32_t t, uint32_t n) {
+    const uint32_t nch = chunks(n);
     bf.bin_start[t] = pn;
     bf.chunk_off[t] = pc;
     for (uint32_t k = 0; k < nch; ++k) bf.chunk_tile[pc + k] = t;
     pn += n;
     pc += nch;
+  };
+  if (per <= PB) {
+#pragma unroll
+    for (uint32_t k = 0; k < PB; ++k)
+      if (t0 + k < t1) place(t0 + k, nv[k]);
+  } else {
+    for (uint32_t t = t0; t < t1; ++t) place(t, bf.tile_n[t]);
   }
-  if (threadIdx.x == 0) {
-    bf.bin_start[T] = tot_n;
-    bf.chunk_off[T] = tot_c;
+  if (tb == T && threadIdx.x == 0) {
+    bf.bin_start[T] = bn + tot_n;
+    bf.chunk_off[T] = bc + tot_c;
   }
 }
 
@@ -1183,7 +1229,7 @@ hipError_t run_bwd_t(const BwdPlan& pl, const BwdGeom* host_geom, const GeomArgs
       blocks = blocks > lb ? blocks : (uint32_t)(lb < 8192 ? lb : 8192);
     }
     blocks = blocks < 1 ? 1 : (blocks > 8192 ? 8192 : blocks);
-    hipLaunchKernelGGL((bwd_round_kernel<EV, EC, VEC>), dim3(blocks), dim3(kBlock), 0, s, bf, n,
+    hipLaunchKernelGGL((bwd_round_kernel<EV, EC, VEC>), dim3(blocks), dim3(kBlock), 0, s, pl, bf, n,
                        pl.grad_loc_elems, DIM);
     if (pl.static_atomic) return hipGetLastError();
   }
@@ -1215,7 +1261,7 @@ hipError_t run_bwd_t(const BwdPlan& pl, const BwdGeom* host_geom, const GeomArgs
   const uint32_t waves_per_block = kBlock / kWave;
   hipLaunchKernelGGL(bwd_colscan_kernel, dim3((pl.T_cap + waves_per_block - 1) / waves_per_block),
                      dim3(kBlock), 0, s, pl, bf);
-  hipLaunchKernelGGL(bwd_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, pl, bf);
+  hipLaunchKernelGGL(bwd_plan_kernel, dim3(pl.groups), dim3(kPlanThreads), 0, s, pl, bf);
   const size_t fill_bytes = 2 * hist_bytes +
                             (size_t)kFillStage * (DIM + 3) * sizeof(uint32_t) +
                             (kBlock / kWave) * sizeof(uint32_t);
@@ -1288,6 +1334,7 @@ BwdSizes bwd_sizes(const BwdPlan& pl, uint64_t samples, int dim) {
   const bool binned = !pl.static_atomic;
   const bool sums = pl.static_atomic || pl.fallback;
   z.counts = binned ? (uint64_t)pl.groups * pl.wgpg * pl.bins_cap : 0u;
+  z.tile_n = (uint64_t)pl.T_cap + 1;
   z.bin_start = (uint64_t)pl.T_cap + 1;
   z.chunk_off = (uint64_t)pl.T_cap + 1;
   z.chunk_tile = pl.max_chunks;
@@ -1296,10 +1343,10 @@ BwdSizes bwd_sizes(const BwdPlan& pl, uint64_t samples, int dim) {
   // atomic path: one fp32 sum per grad_value element of a launch (groups << hg_log2 =
   // batches * H)
   z.sum_floats = sums ? ((uint64_t)pl.groups << pl.hg_log2) * (uint64_t)pl.K * pl.C : 0u;
-  z.value_h_bytes = pl.head_major ? (uint64_t)pl.value_bytes : 0u;
+  z.value_h_bytes = pl.head_major && !pl.hm_given ? (uint64_t)pl.value_bytes : 0u;
   z.geom_bytes = sizeof(BwdGeom);
   auto al = [](uint64_t b) { return (b + 255) & ~(uint64_t)255; };
-  z.total_bytes = al(z.counts * 4) + al(z.bin_start * 4) + al(z.chunk_off * 4) +
+  z.total_bytes = al(z.counts * 4) + al(z.tile_n * 4) + al(z.bin_start * 4) + al(z.chunk_off * 4) +
                   al(z.chunk_tile * 4) + al(z.record_words * 4) + al(z.scratch_floats * 4) +
                   al(z.sum_floats * 4) + al(z.value_h_bytes) + al(z.geom_bytes);
   return z;

@@ -228,6 +228,8 @@ struct BwdPlan {
   int32_t clamp;
   int32_t coords_aligned;      // loc and attn are 16-byte aligned: per-batch block loads allowed
   int32_t head_major;          // the sample-gradient kernel reads BwdBuffers::value_h
+  int32_t hm_given;            // value_h is the caller's head-major value (no relayout, no
+                               // workspace for it)
   int32_t static_atomic;       // the host chose the atomic path (levels beyond the LDS binning,
                                // or sample ids beyond a record): grad_value is scattered with
                                // fp32 atomics into BwdBuffers::sums, then rounded into grad_value
@@ -256,17 +258,18 @@ struct BwdBuffers {
   void* grad_loc;
   void* grad_attn;
   uint32_t* counts;      // (groups * bins) x wgpg: per-(tile, bin workgroup) counts -> offsets
-  uint32_t* bin_start;   // T + 1: record totals -> first record of each tile
+  uint32_t* tile_n;      // T: record total of each tile (column scan -> plan)
+  uint32_t* bin_start;   // T + 1: first record of each tile
   uint32_t* chunk_off;   // T + 1: first chunk of each tile; [T] = number of chunks
   uint32_t* chunk_tile;  // max_chunks: tile of each chunk
   uint32_t* records;     // (DIM + 2) words per record: id | flags, u_x, u_y[, u_z], attn
   float* scratch;        // max_chunks * rcells * C fp32 partials
-  float* sums;           // atomic path: (Bc, K, H, C) fp32 sums
+  float* sums;           // atomic path: fp32 sums in the gathered value's layout
   const BwdGeom* geom;   // level geometry of the launch (written by the first kernel)
 };
 
 struct BwdSizes {
-  uint64_t counts, bin_start, chunk_off, chunk_tile, record_words, scratch_floats, sum_floats;
+  uint64_t counts, tile_n, bin_start, chunk_off, chunk_tile, record_words, scratch_floats, sum_floats;
   uint64_t value_h_bytes;  // head-major value copy (0 when the plan does not use one)
   uint64_t geom_bytes;
   uint64_t total_bytes;

@@ -12,7 +12,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libmsda_hip.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 MSDA_F32, MSDA_F16, MSDA_BF16 = 0, 1, 2
 MSDA_OK, MSDA_ERR_INVALID, MSDA_ERR_DTYPE, MSDA_ERR_WORKSPACE, MSDA_ERR_HIP = range(5)
@@ -35,6 +35,7 @@ EXPORTED_SYMBOLS = (
     "msda_bwd_noalloc",
 )
 NOALLOC_SCRATCH_BYTES = 256 << 20  # MSDA_NOALLOC_SCRATCH_BYTES
+FLAG_VALUE_HEAD_MAJOR = 1  # MSDA_FLAG_VALUE_HEAD_MAJOR
 
 
 class MsdaDesc(ctypes.Structure):
@@ -52,7 +53,7 @@ class MsdaDesc(ctypes.Structure):
         ("value_dtype", ctypes.c_int32),
         ("coord_dtype", ctypes.c_int32),
         ("clamp_grid", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("flags", ctypes.c_int32),
         ("clamp_eps", ctypes.c_double),
     ]
 

@@ -231,7 +231,7 @@ def make_desc(dim: int, value: torch.Tensor, loc: torch.Tensor, cdt: torch.dtype
     d.value_dtype = _DTYPE_CODE[value.dtype]
     d.coord_dtype = _DTYPE_CODE[cdt]
     d.clamp_grid = 1 if clamp_grid else 0
-    d.reserved = 0
+    d.flags = 0
     d.clamp_eps = float(clamp_eps)
     return d
 
@@ -258,8 +258,10 @@ def _stream(device: torch.device) -> int:
 
 def forward(dim: int, value: torch.Tensor, levels: Levels, loc: torch.Tensor, attn: torch.Tensor,
             clamp_grid: bool, clamp_eps: float):
-    """Launch msda_fwd. Returns (out, value_c, loc_c, attn_c): the output and the
-    contiguous, kernel-dtype inputs it read (saved for backward)."""
+    """Launch msda_fwd. Returns (out, value_c, loc_c, attn_c, value_hm): the output, the
+    contiguous, kernel-dtype inputs it read (saved for backward) and the head-major copy of
+    the whole value the kernel gathered from (its workspace), or None when it made none or
+    only of one batch chunk."""
     lib = _lib.load()
     cdt = coord_dtype(value, loc, attn)
     value_c = _aligned(value.contiguous())
@@ -278,13 +280,16 @@ def forward(dim: int, value: torch.Tensor, levels: Levels, loc: torch.Tensor, at
                           out.data_ptr(), ws.data_ptr() if ws is not None else None, ws_bytes,
                           _stream(value.device))
     _lib.check(rc, "msda_fwd")
-    return out, value_c, loc_c, attn_c
+    whole = ws is not None and ws_bytes == value_c.numel() * value_c.element_size()
+    return out, value_c, loc_c, attn_c, (ws if whole else None)
 
 
 def backward(dim: int, grad_output: torch.Tensor, value_c: torch.Tensor, levels: Levels,
-             loc_c: torch.Tensor, attn_c: torch.Tensor, clamp_grid: bool, clamp_eps: float):
+             loc_c: torch.Tensor, attn_c: torch.Tensor, clamp_grid: bool, clamp_eps: float,
+             value_hm: torch.Tensor | None = None):
     """Launch msda_bwd. Returns (grad_value, grad_loc, grad_attn) in the kernel dtypes,
-    all freshly allocated and contiguous."""
+    all freshly allocated and contiguous. value_hm: the forward's head-major copy of value_c
+    (then the backward gathers from it and makes no copy of its own)."""
     lib = _lib.load()
     grad_out = _aligned(grad_output.to(dtype=value_c.dtype).contiguous())
     value_c = _aligned(value_c)
@@ -292,6 +297,10 @@ def backward(dim: int, grad_output: torch.Tensor, value_c: torch.Tensor, levels:
     grad_loc = torch.empty(loc_c.shape, device=loc_c.device, dtype=loc_c.dtype)
     grad_attn = torch.empty(attn_c.shape, device=attn_c.device, dtype=attn_c.dtype)
     desc = make_desc(dim, value_c, loc_c, loc_c.dtype, clamp_grid, clamp_eps)
+    value_ptr = value_c.data_ptr()
+    if value_hm is not None:
+        desc.flags = _lib.FLAG_VALUE_HEAD_MAJOR
+        value_ptr = value_hm.data_ptr()
     if levels.host is not None:
         # CPU-resident shapes: the host plans every size exactly
         name, shapes = "msda_bwd", levels.host.data_ptr()
@@ -306,7 +315,7 @@ def backward(dim: int, grad_output: torch.Tensor, value_c: torch.Tensor, levels:
         _lib.check(_lib.MSDA_ERR_INVALID, name + "_workspace_bytes")
     ws = torch.empty(max(ws_bytes, 1), device=value_c.device, dtype=torch.uint8)
     with _on_device(value_c.device):
-        rc = entry(ctypes.byref(desc), shapes, value_c.data_ptr(), loc_c.data_ptr(),
+        rc = entry(ctypes.byref(desc), shapes, value_ptr, loc_c.data_ptr(),
                    attn_c.data_ptr(), grad_out.data_ptr(), grad_value.data_ptr(),
                    grad_loc.data_ptr(), grad_attn.data_ptr(), ws.data_ptr(), ws_bytes,
                    _stream(value_c.device))
@@ -319,9 +328,12 @@ def fn_forward(ctx, name: str, dim: int, value, value_spatial_shapes, sampling_l
     """Body of MSDA2DFn.forward / MSDA3DFn.forward (reference triton/msda_2d.py:749-775)."""
     validate_inputs(name, dim, value, value_spatial_shapes, sampling_locations, attention_weights)
     levels = prepare_levels(dim, value, value_spatial_shapes)
-    out, value_c, loc_c, attn_c = forward(dim, value, levels, sampling_locations,
-                                          attention_weights, clamp_grid, clamp_eps)
+    out, value_c, loc_c, attn_c, value_hm = forward(dim, value, levels, sampling_locations,
+                                                    attention_weights, clamp_grid, clamp_eps)
     ctx.save_for_backward(value_c, loc_c, attn_c)
+    # the head-major copy the forward gathered from serves the backward too (one relayout
+    # per training step instead of two); a workspace, not an input or output of the op
+    ctx.value_hm = value_hm if any(ctx.needs_input_grad) else None
     ctx.levels = levels
     ctx.clamp_grid = clamp_grid
     ctx.clamp_eps = clamp_eps
@@ -334,7 +346,8 @@ def fn_backward(ctx, dim: int, grad_output: torch.Tensor):
     returns (grad_value, None, grad_loc, grad_attn, None, None) in the input dtypes."""
     value_c, loc_c, attn_c = ctx.saved_tensors
     gv, gl, ga = backward(dim, grad_output, value_c, ctx.levels, loc_c, attn_c,
-                          ctx.clamp_grid, ctx.clamp_eps)
+                          ctx.clamp_grid, ctx.clamp_eps, ctx.value_hm)
+    ctx.value_hm = None
     vdt, ldt, adt = ctx.in_dtypes
     return gv.to(vdt), None, gl.to(ldt), ga.to(adt), None, None
 
@@ -344,6 +357,6 @@ def run_fwd(name: str, dim: int, value, value_spatial_shapes, sampling_locations
     """Forward-only entry (msda2d_fwd / msda3d_fwd)."""
     validate_inputs(name, dim, value, value_spatial_shapes, sampling_locations, attention_weights)
     levels = prepare_levels(dim, value, value_spatial_shapes)
-    out, _, _, _ = forward(dim, value, levels, sampling_locations, attention_weights, clamp_grid,
-                           clamp_eps)
+    out = forward(dim, value, levels, sampling_locations, attention_weights, clamp_grid,
+                  clamp_eps)[0]
     return out

@@ -35,7 +35,7 @@ def _desc(**kw):
     d = _lib.MsdaDesc()
     base = dict(dim=2, batch=2, num_keys=19947, num_heads=8, channels=32, num_queries=19947,
                 num_levels=4, num_points=4, value_dtype=_lib.MSDA_BF16,
-                coord_dtype=_lib.MSDA_BF16, clamp_grid=1, reserved=0, clamp_eps=1e-4)
+                coord_dtype=_lib.MSDA_BF16, clamp_grid=1, flags=0, clamp_eps=1e-4)
     base.update(kw)
     for k, v in base.items():
         setattr(d, k, v)
@@ -86,7 +86,12 @@ def test_validate_status_codes():
     assert v(value_dtype=_lib.MSDA_BF16, coord_dtype=_lib.MSDA_F32) == _lib.MSDA_OK
     assert v(num_keys=2**31) == _lib.MSDA_ERR_INVALID and "int32" in _lib.last_error()
     assert v(num_levels=65) == _lib.MSDA_ERR_INVALID
-    assert v(reserved=1) == _lib.MSDA_ERR_INVALID
+    # flags: only the head-major value bit is known, and it is valid for the backward alone
+    assert v(flags=2) == _lib.MSDA_ERR_INVALID and "unknown flags" in _lib.last_error()
+    assert v(flags=_lib.FLAG_VALUE_HEAD_MAJOR) == _lib.MSDA_OK
+    hm = _desc(flags=_lib.FLAG_VALUE_HEAD_MAJOR)
+    assert lib.msda_fwd_workspace_bytes(ctypes.byref(hm)) == 0
+    assert "backward only" in _lib.last_error()
     assert v(clamp_eps=float("nan")) == _lib.MSDA_ERR_INVALID
     assert v(num_heads=0) == _lib.MSDA_ERR_INVALID
     # one batch's fp32 view of value must stay below 2^31 bytes
@@ -113,7 +118,14 @@ def test_bwd_workspace_bytes_host_only():
     # 3D, the 4-level volumetric configuration
     d3 = _desc(dim=3, batch=1, num_keys=149760, num_queries=32768, num_points=8)
     s3 = (32, 64, 64, 16, 32, 32, 8, 16, 16, 4, 8, 8)
-    assert lib.msda_bwd_workspace_bytes(ctypes.byref(d3), _shapes(s3)) > 0
+    n3 = lib.msda_bwd_workspace_bytes(ctypes.byref(d3), _shapes(s3))
+    assert n3 > 0
+    # a caller-supplied head-major value (the forward's copy): the relayout's workspace,
+    # the whole value (149760 * 8 * 32 bf16), is no longer needed
+    h3 = _desc(dim=3, batch=1, num_keys=149760, num_queries=32768, num_points=8,
+               flags=_lib.FLAG_VALUE_HEAD_MAJOR)
+    assert lib.msda_fwd_workspace_bytes(ctypes.byref(d3)) == 149760 * 8 * 32 * 2
+    assert n3 - lib.msda_bwd_workspace_bytes(ctypes.byref(h3), _shapes(s3)) == 149760 * 8 * 32 * 2
 
 
 def test_bwd_levels_beyond_binning_plan_atomic_path():

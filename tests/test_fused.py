@@ -121,7 +121,7 @@ def _desc(**kw):
     d = _lib.MsdaDesc()
     base = dict(dim=2, batch=2, num_keys=19947, num_heads=8, channels=32, num_queries=19947,
                 num_levels=4, num_points=4, value_dtype=_lib.MSDA_BF16,
-                coord_dtype=_lib.MSDA_BF16, clamp_grid=1, reserved=0, clamp_eps=1e-4)
+                coord_dtype=_lib.MSDA_BF16, clamp_grid=1, flags=0, clamp_eps=1e-4)
     base.update(kw)
     for k, v in base.items():
         setattr(d, k, v)

@@ -84,3 +84,54 @@ def test_head_major_parity(dim, dtype, ch, tol):
     assert max_rel(out.detach().float().cpu(), ref) <= fwd_tol
     assert max_rel(v.grad.float().cpu(), tv) <= tol
     assert max_rel(a.grad.float().cpu(), ta) <= tol
+
+
+def _bwd(dim, value, shapes, loc, attn, grad_out, given_hm):
+    """_core.backward on the GPU, with the value's head-major copy supplied by the caller
+    (MSDA_FLAG_VALUE_HEAD_MAJOR) or not."""
+    dev = torch.device("cuda")
+    v, lo, a, g = (t.to(dev).contiguous() for t in (value, loc, attn, grad_out))
+    levels = _core.prepare_levels(dim, v, shapes)
+    hm = v.permute(0, 2, 1, 3).contiguous() if given_hm else None
+    gv, gl, ga = _core.backward(dim, g, v, levels, lo, a, True, 1e-4, value_hm=hm)
+    return gv.cpu(), gl.cpu(), ga.cpu()
+
+
+def _same_grads(x, y, tol):
+    """grad_loc and grad_attn come from the same per-sample arithmetic: equal bit for bit;
+    grad_value sums the same terms, in an order that LDS atomics (binned path) or global
+    atomics (atomic path) do not fix."""
+    assert torch.equal(x[1], y[1]) and torch.equal(x[2], y[2])
+    assert max_rel(x[0].float(), y[0].float()) <= tol
+
+
+@pytest.mark.parametrize("dim,dtype,tol", [(2, torch.bfloat16, 1e-2), (3, torch.bfloat16, 1e-2),
+                                           (2, torch.float32, 1e-6)])
+def test_backward_from_caller_head_major_value(dim, dtype, tol):
+    """A caller-supplied head-major value (what the autograd function passes on from the
+    forward's workspace) gives the gradients of the backward's own relayout."""
+    value, shapes, loc, attn = _case(dim, dtype, 32 if dtype != torch.float32 else 16)
+    grad_out = torch.randn(value.shape[0], loc.shape[1], value.shape[2] * value.shape[3],
+                           generator=torch.Generator().manual_seed(9)).to(dtype)
+    print(f"caller head-major dim={dim} {dtype}", flush=True)
+    _same_grads(_bwd(dim, value, shapes, loc, attn, grad_out, True),
+                _bwd(dim, value, shapes, loc, attn, grad_out, False), tol)
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+def test_caller_head_major_value_on_small_and_atomic_plans(dim):
+    """The flag also holds where the backward would not relayout itself: a small pyramid (the
+    plan then keeps one head per group) and levels beyond the LDS binning (atomic path: the
+    fp32 sums follow the head-major layout and the rounding pass transposes them back)."""
+    if dim == 2:
+        cases = [dict(ss=[(32, 32), (16, 16)], q=100, b=1), dict(ss=[(1032, 1024), (3, 5)], q=64, b=2)]
+    else:
+        cases = [dict(ss=[(8, 8, 8), (4, 4, 4)], q=100, b=1), dict(ss=[(72, 128, 128), (3, 5, 1)], q=64, b=1)]
+    for c in cases:
+        value, shapes, loc, attn = make_inputs(dim, batch_size=c["b"], num_queries=c["q"], num_heads=2,
+                                               dim_per_head=32, num_levels=len(c["ss"]), num_points=4,
+                                               spatial_shapes=c["ss"])
+        grad_out = torch.randn(c["b"], c["q"], 2 * 32, generator=torch.Generator().manual_seed(3))
+        print(f"caller head-major dim={dim} shapes={c['ss']}", flush=True)
+        _same_grads(_bwd(dim, value, shapes, loc, attn, grad_out, True),
+                    _bwd(dim, value, shapes, loc, attn, grad_out, False), 1e-5)

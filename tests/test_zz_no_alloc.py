@@ -83,7 +83,7 @@ def test_noalloc_refuses_problems_beyond_the_scratch():
     d = _lib.MsdaDesc()
     for k, v in dict(dim=3, batch=1, num_keys=149760, num_heads=8, channels=32,
                      num_queries=32768, num_levels=4, num_points=8, value_dtype=_lib.MSDA_BF16,
-                     coord_dtype=_lib.MSDA_BF16, clamp_grid=1, reserved=0,
+                     coord_dtype=_lib.MSDA_BF16, clamp_grid=1, flags=0,
                      clamp_eps=1e-4).items():
         setattr(d, k, v)
     hs = torch.tensor([32, 64, 64, 16, 32, 32, 8, 16, 16, 4, 8, 8], dtype=torch.int32)
