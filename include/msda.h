@@ -75,9 +75,9 @@ typedef struct msda_desc {
  * workspace queries reject it): `value` points to a head-major (B, H, K, C) copy of the
  * value tensor instead of the (B, K, H, C) tensor itself, such as the copy msda_fwd leaves
  * at the start of its workspace when msda_fwd_workspace_bytes() equals the whole value's
- * bytes. The backward then gathers from it directly and makes no copy of its own (the 3D
- * 4-level training step saves one 25 us relayout and 77 MB of workspace). The caller keeps
- * the copy alive and unchanged until the backward has run. No counterpart in the reference.
+ * bytes. The backward then reads value rows in that layout (it never copies value, so the
+ * flag only spares the caller from keeping the original tensor). The caller keeps the copy
+ * alive and unchanged until the backward has run. No counterpart in the reference.
  */
 #define MSDA_FLAG_VALUE_HEAD_MAJOR 1
 

@@ -40,11 +40,8 @@ const char* dtype_name(int dt) {
 
 constexpr uint64_t kLim31 = 0x7FFFFFFFull;
 constexpr uint32_t kChunkRecords = 4096;        // records per tile-kernel chunk (rounded to S)
-// LDS share of one tile workgroup at the kernel's occupancy target (160 KB LDS per CU):
-// four workgroups in 2D, two in 3D
-constexpr uint32_t kTileLdsTarget2 = 40 * 1024 - 256;
-constexpr uint32_t kTileLdsTarget3 = 80 * 1024 - 256;
-constexpr uint32_t kTileLdsBudget = 160 * 1024 - 256;  // one workgroup per CU
+// LDS share of one tile workgroup when n of them share a CU (160 KB LDS per CU)
+constexpr uint32_t tile_lds_share(uint32_t n) { return 160u * 1024u / n - 256u; }
 constexpr int kMaxBinsLds = 8192;  // bin histogram + bases in 64 KB of LDS
 
 // The current device's compute units, XCDs and per-XCD L2 bytes, which size the staged
@@ -270,11 +267,21 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
   // Tile extents and sub-batch size: start from 16x16 (2D) / 8x8x8 (3D) cells and
   // S = kTileThreads<dim> records (one per thread); halve the largest tile extent until a thread
   // owns at most kTileMaxItems (region cell, owner chunk) items, and lower S in steps of
-  // half a wave until the sub-batch's fp32 grad_out rows, sorted entries and two counter sets
-  // fit the LDS share of one workgroup at the occupancy target (or, for very wide heads, all of a
-  // CU's LDS).
+  // half a wave until the sub-batch's grad_out rows, sorted entries, two counter sets and the
+  // region's value rows fit the LDS share of one workgroup. Fewer records per sub-batch cost
+  // more than fewer workgroups per CU (C2 tile kernel: S = 160 at four workgroups per CU
+  // 213 us, S = 224 161 us), so S stays at half the threads or more: the LDS share is that
+  // of four, three or two workgroups per CU (2D; two in 3D), then of one, and only then do
+  // the tiles shrink for LDS.
   const uint32_t NT = d->dim == 2 ? msda::kTileThreads<2> : msda::kTileThreads<3>;
-  const uint32_t grow = (uint32_t)d->channels * 4u;
+  // 16-bit values: the tile kernel forms the sample gradients from staged region rows
+  const bool tile_dots = s == 2;
+  // staged rows (grad_out and value, both in the value dtype): with tile_dots C * s rounded
+  // up to an odd number of 16-byte slots, so one chunk of random rows spreads over every
+  // bank slot
+  const uint32_t grow = tile_dots ? ((uint32_t)(d->channels * s) + 15u) / 32u * 32u + 16u
+                                  : (uint32_t)(d->channels * s);
+  const uint32_t vrow = tile_dots ? grow : 0u;
   const int onv = d->channels / msda::tile_owner_vec(lay.vec_bytes / s);
   int T[3];
   uint32_t S = NT, lds = 0;
@@ -285,8 +292,9 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
     T[k] /= 2;
     return true;
   };
-  // largest tile, then largest S, that meets the per-thread limit and the LDS budget
-  auto fit = [&](uint32_t budget) {
+  // largest tile, then largest S >= smin, that meets the per-thread limit and the LDS
+  // budget; shrink: smaller tiles when no S fits
+  auto fit = [&](uint32_t budget, uint32_t smin, bool shrink_for_lds) {
     T[0] = T[1] = 16;
     T[2] = 1;
     if (d->dim == 3) T[0] = T[1] = T[2] = 8;
@@ -299,7 +307,8 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
         if (!shrink()) return false;
         continue;
       }
-      lds = S * grow + S * nc * 8u + 2u * (uint32_t)((rcells + 4) & ~3) * 4u;
+      lds = S * grow + S * nc * 8u + 2u * (uint32_t)((rcells + 4) & ~3) * 4u +
+            (uint32_t)rcells * vrow;
       // a corner's (cell, rank) pair is packed into 16 + 16 bits
       if (rcells >= (1 << 16) || S * nc >= (1u << 16)) {
         if (!shrink()) return false;
@@ -307,15 +316,23 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
       }
       if (lds <= budget) return true;
       // (steps of 32 records: C2 S = 224 against 192 in steps of 64, backward 358 -> 348 us)
-      if (S > 32u) {
+      if (S >= smin + 32u) {
         S -= 32u;
         continue;
       }
-      if (!shrink()) return false;
+      if (!shrink_for_lds || !shrink()) return false;
       S = NT;
     }
   };
-  if (!fit(d->dim == 2 ? kTileLdsTarget2 : kTileLdsTarget3) && !fit(kTileLdsBudget))
+  bool planned = false;
+  if (d->dim == 2) {
+    for (uint32_t wgs = 4; wgs >= 2 && !planned; --wgs)
+      planned = fit(tile_lds_share(wgs), NT / 2, false);
+  } else {
+    planned = fit(tile_lds_share(2), NT / 2, false);
+  }
+  if (!planned) planned = fit(tile_lds_share(1), 32u, true);
+  if (!planned)
     return fail(MSDA_ERR_INVALID, "channels per head (%d) too large for the backward", d->channels);
   pl.TX = T[0];
   pl.TY = T[1];
@@ -339,13 +356,16 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
   pl.cells = T[0] * T[1] * T[2];
   pl.rcells = rcells;
   pl.S = S;
+  pl.tile_dots = tile_dots ? 1 : 0;
+  pl.grow = grow;
+  pl.vrow = vrow;
   pl.lds_g_bytes = S * grow;
   pl.lds_bytes = lds;
   // Tiles per head over all levels: exact from host shapes, else an estimate from K.
   // Levels with more than kMaxBinsLds tiles per head do not fit the LDS binning of the
-  // sample-gradient and fill kernels, and more than 2^27 samples per (b, h, level) do not fit
-  // a record id: such plans scatter grad_value with fp32 atomics instead (sample-gradient
-  // kernel only, then one rounding pass).
+  // count and fill kernels, and more than 2^27 samples per (b, h, level) do not fit a record
+  // id: such plans scatter grad_value with fp32 atomics instead (atomic kernel, then one
+  // rounding pass).
   int64_t tiles = 0;
   for (int l = 0; l < d->num_levels && !dev; ++l) {
     const int32_t* r = hs + l * d->dim;
@@ -358,14 +378,12 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
   pl.static_atomic = atomic ? 1 : 0;
   pl.fallback = dev && !atomic ? 1 : 0;
   if (atomic) tiles = 0;
-  // value already head-major (MSDA_FLAG_VALUE_HEAD_MAJOR): gather from it, copy nothing
-  const bool hm_given = (d->flags & MSDA_FLAG_VALUE_HEAD_MAJOR) != 0;
-  const bool head_major = hm_given || (!atomic && use_head_major(d));
+  // value already head-major (MSDA_FLAG_VALUE_HEAD_MAJOR): read it in that layout
+  const bool head_major = (d->flags & MSDA_FLAG_VALUE_HEAD_MAJOR) != 0;
   // Heads whose rows share 128-byte lines are grouped (their units and chunks run on one
-  // XCD). A head-major copy shares no lines across heads: one head per group then keeps
-  // one head's value and grad_out rows per XCD (C5: tile 699 -> 523 us, sample gradients
-  // 465 -> 449 us, fill 110 -> 105 us).
-  int hg = head_major ? 0 : lay.hg_log2;
+  // XCD). Where a head's keys exceed an XCD's L2 (the forward's head-major rule), one head
+  // per group keeps one head's grad_out rows per XCD instead (C5: tile 699 -> 523 us).
+  int hg = head_major || (!atomic && use_head_major(d)) ? 0 : lay.hg_log2;
   while (hg > 0 && (tiles << hg) > kMaxBinsLds) --hg;
   const int64_t bins_cap = (tiles << hg) < kMaxBinsLds ? (tiles << hg) : kMaxBinsLds;
   pl.L = d->num_levels;
@@ -378,7 +396,6 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
   pl.div_lp = msda::make_fastdiv((uint32_t)(d->num_levels * d->num_points > 0
                                                 ? d->num_levels * d->num_points : 1));
   pl.head_major = head_major ? 1 : 0;
-  pl.hm_given = hm_given ? 1 : 0;
   pl.hg_log2 = hg;
   pl.bins_cap = (int32_t)bins_cap;
   pl.upw = (msda::kGradThreads >> lay.lpu_log2) * msda::kGradRounds;
@@ -452,8 +469,6 @@ void carve(char* ws, const msda::BwdSizes& z, msda::BwdBuffers* bf) {
   bf->scratch = reinterpret_cast<float*>(p);
   p += al(z.scratch_floats * 4);
   bf->sums = reinterpret_cast<float*>(p);
-  p += al(z.sum_floats * 4);
-  bf->value_h = z.value_h_bytes ? p : nullptr;
 }
 
 // Body of msda_fwd and msda_fwd_fused. fused: `loc` / `attn` are the sampling offsets and
@@ -669,14 +684,6 @@ int bwd_impl(const msda_desc* d, const int32_t* hs, const int32_t* ds, const voi
     bf.grad_attn = static_cast<char*>(grad_attention_weights) + (uint64_t)b0 * qh * LP * sc;
     pl.coords_aligned = aligned(bf.loc, 16) && aligned(bf.attn, 16) && aligned(bf.grad_loc, 16) &&
                         aligned(bf.grad_attn, 16);
-    if (pl.hm_given) {
-      bf.value_h = bf.value;  // this launch's batches of the caller's head-major copy
-    } else if (pl.head_major) {
-      hipError_t e = msda::launch_head_major(bf.value, const_cast<void*>(bf.value_h), (uint32_t)bc,
-                                             (uint32_t)d->num_keys, (uint32_t)d->num_heads,
-                                             (uint32_t)(d->channels * sv), hp.lay.vec_bytes, st);
-      if (e != hipSuccess) return fail(MSDA_ERR_HIP, "%s relayout failed: %s", name, hipGetErrorString(e));
-    }
     hipError_t e = msda::run_bwd(pl, hs ? &geom : nullptr, hs ? nullptr : &ga, ds, bf, d->dim,
                                  d->value_dtype, d->coord_dtype, hp.lay.vec_bytes, st);
     if (e != hipSuccess) return fail(MSDA_ERR_HIP, "%s launch failed: %s", name, hipGetErrorString(e));

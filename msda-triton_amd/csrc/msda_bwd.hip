@@ -7,39 +7,43 @@
 // random rows sustain about 0.33 T element-adds/s and LDS fp32 atomics about a third of
 // an operation per clock per CU, so this backward accumulates grad_value in key order:
 //
-//  1. sample gradients + count: one lane group per unit (b, q, h), as in the forward:
-//     the unit's grad_out row is read once into registers, each sample's corner rows are
-//     gathered from L2 (value slices stay XCD-resident) and grad_attention_weights and
-//     grad_sampling_locations are stored per unit. Every sample with a valid corner is
-//     also assigned to the tile of its level that owns its lowest corner; each workgroup
-//     (upw units of one (batch, head-group)) histograms its samples per tile in LDS
-//     (integer atomics, full rate) and writes the histogram as one column of a tile-major
-//     (tile, workgroup) count matrix.
+//  1. count: every sample with a valid corner is assigned, from its coordinates alone, to
+//     the tile of its level that owns its lowest corner; each workgroup (upw units of one
+//     (batch, head-group)) histograms its samples per tile in LDS (integer atomics, full
+//     rate) and writes the histogram as one column of a tile-major (tile, workgroup)
+//     count matrix.
 //  2. column scan (one wave per tile): the tile's counts over the workgroups become
 //     offsets within the tile, and the tile's total.
 //  3. plan (one workgroup): exclusive scan of the tile totals, chunks of at most R records
 //     per tile, and the chunk -> tile table.
-//  4. fill: per level, each workgroup ranks its samples per tile in LDS, sorts their
-//     records (id, clamp flags, pixel coordinates, attention weight) by tile in LDS and
-//     writes them out as contiguous runs.
+//  4. fill: each workgroup ranks its samples per tile in LDS, sorts their records (id,
+//     clamp flags, pixel coordinates, attention weight) by tile in LDS and writes them out
+//     as contiguous runs.
 //  5. tile kernel: one workgroup per chunk, chunks of one (batch, head-group) on one XCD.
-//     Per sub-batch of S records it stages the records and their grad_out rows (two
-//     coalesced round trips), sorts the (corner weight * attn, record) entries by cell of
-//     the tile's region (the tile plus a one-cell high-side halo, which holds every corner
-//     of a sample anchored in the tile; ranks come from the counting atomics), and
-//     accumulates grad_value for every region cell in the fp32 registers of the cell's
-//     owner threads. Interior cells of a one-chunk tile are written directly in the value
-//     dtype; edge cells (which also receive halo contributions of lower neighbours), halo
-//     cells and every cell of a split tile are written as fp32 partials.
+//     It stages the value rows of the tile's region (the tile plus a one-cell high-side
+//     halo, which holds every corner of a sample anchored in the tile) in LDS once. Per
+//     sub-batch of S records it stages the records and their grad_out rows, forms each
+//     record's corner dot products <grad_out, v_c> from LDS and stores the sample's
+//     grad_attention_weights and clamp-masked grad_sampling_locations, sorts the
+//     (corner weight * attn, record) entries by region cell (ranks come from the counting
+//     atomics), and accumulates grad_value for every region cell in the fp32 registers of
+//     the cell's owner threads. Interior cells of a one-chunk tile are written directly in
+//     the value dtype; edge cells (which also receive halo contributions of lower
+//     neighbours), halo cells and every cell of a split tile are written as fp32 partials.
 //  6. fold: per tile, sums the partials of its own chunks and the halo partials of its
 //     lower neighbours' chunks, in a fixed order, and writes the edge / split cells.
+//
+// Gathering the corner rows per sample (in query order, from L2) cost more than staging
+// each tile's rows once: C2 bf16 sample gradients 106 us against an 11 us count pass plus
+// 80 us more in the tile kernel; C5 350 us against 27 + 260 us.
 //
 // Every grad_value element is written exactly once with a plain store, so no clearing
 // pass is needed and 16-bit values are rounded once, from fp32.
 //
 // Pyramids beyond the LDS binning (more than kMaxBinsLds tiles per head) and launches whose
-// Q * P exceeds a record's 27-bit sample id run step 1 alone with global fp32 atomics into
-// fp32 sums in the workspace, then one rounding pass.
+// Q * P exceeds a record's 27-bit sample id instead gather each sample's corner rows per
+// unit and scatter grad_value with global fp32 atomics into fp32 sums in the workspace,
+// then round them in one pass.
 #include "msda_internal.h"
 #include "msda_sample.h"
 
@@ -195,7 +199,7 @@ __device__ inline bool sample_tile(const BwdPlan& pl, const BwdLevel& lv, const 
   return true;
 }
 
-// ------------------------------------------------------------------ 1: sample gradients
+// ------------------------------------------------------------------ atomic path
 // Gradients of one sample from its gathered corner rows: <grad_out, v_c> per corner, then
 // d/d(attn) and (clamp-masked) d/d(loc) summed over the unit's lanes, so every lane of
 // the group holds them. out = {grad_attn, grad_loc x, y[, z]}.
@@ -326,8 +330,8 @@ __global__ __launch_bounds__(kGradThreads) void bwd_grad_kernel(const BwdPlan pl
   const uint32_t units = min((uint32_t)pl.upw, (pl.Q << pl.hg_log2) - w * (uint32_t)pl.upw);
   const int LP = pl.L * pl.P;
   const bool hm = pl.head_major != 0;
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc(hm ? bf.value_h : bf.value, pl.value_bytes);
-  // bytes between rows of K: one head's rows are contiguous in the head-major copy
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(bf.value, pl.value_bytes);
+  // bytes between rows of K: one head's rows are contiguous in the head-major layout
   const uint32_t rs = (hm ? 1u : (uint32_t)pl.H) * (uint32_t)pl.C * EV::kBytes;
 #pragma unroll 1
   for (uint32_t wi = threadIdx.x >> lg; wi < units; wi += gpw) {
@@ -472,6 +476,116 @@ __global__ __launch_bounds__(kGradThreads) void bwd_grad_kernel(const BwdPlan pl
   }
 }
 
+// Binned plans, step 1: count the samples of each (tile, workgroup) from their coordinates
+// alone. Same workgroup -> units mapping as the fill kernel; each workgroup histograms its
+// samples per tile in LDS (integer atomics) and writes the histogram as one column of the
+// tile-major count matrix. A sample with no corner inside its level gets its zero
+// grad_loc and grad_attn here; every other sample's are written by the tile kernel. The
+// geometry: with host shapes (pl.geom_arg) the kernel argument hg, which workgroup 0 also
+// stores in the workspace for the kernels after this one; else the copy bwd_geom_kernel
+// wrote. PT > 0: P is a compile-time constant and each (unit, level) block of coordinates is
+// one vector load (consecutive threads read consecutive blocks); else one scalar load per
+// coordinate.
+template <int DIM, typename EC, int PT>
+__global__ __launch_bounds__(kBlock) void bwd_count_kernel(const BwdPlan pl, const BwdBuffers bf,
+                                                           const BwdGeom hg) {
+  typedef typename EC::T TC;
+  extern __shared__ uint32_t s_hist[];  // [bins]
+  const GeoP geo = pl.geom_arg ? (GeoP)&hg : geo_of(bf);
+  if (pl.geom_arg && blockIdx.x == 0) {
+    BwdGeom* dst = const_cast<BwdGeom*>(bf.geom);
+    for (uint32_t i = threadIdx.x; i < sizeof(BwdGeom) / 4; i += kBlock)
+      reinterpret_cast<uint32_t*>(dst)[i] = reinterpret_cast<const uint32_t*>(&hg)[i];
+  }
+  if (geo->atomic) return;
+  const int bins = geo->bins;
+  const uint32_t lb = xcd_logical_block(blockIdx.x, gridDim.x, pl.xcds);
+  const uint32_t g = lb / (uint32_t)pl.wgpg;
+  const uint32_t w = lb - g * (uint32_t)pl.wgpg;
+  for (int i = threadIdx.x; i < bins; i += kBlock) s_hist[i] = 0;
+  __syncthreads();
+  const uint32_t units = min((uint32_t)pl.upw, (pl.Q << pl.hg_log2) - w * (uint32_t)pl.upw);
+  const int LP = pl.L * pl.P;
+  // sample si of the launch at location xyz on level lv, head hsub of the group
+  auto count = [&](const BwdLevel& lv, const float* xyz, uint32_t hsub, size_t si) {
+    float u[3];
+    uint32_t flags;
+    int tib;
+    if (sample_tile<DIM>(pl, lv, xyz, u, &flags, &tib)) {
+      atomicAdd(&s_hist[((uint32_t)tib << pl.hg_log2) | hsub], 1u);
+    } else {
+      static_cast<TC*>(bf.grad_attn)[si] = (TC)0.0f;
+#pragma unroll
+      for (int d = 0; d < DIM; ++d) static_cast<TC*>(bf.grad_loc)[si * DIM + d] = (TC)0.0f;
+    }
+  };
+  constexpr int NB = 4;  // blocks (or samples) per thread in flight
+  if constexpr (PT > 0) {
+    const uint32_t nblk = units * (uint32_t)pl.L;
+    for (uint32_t b0 = 0; b0 < nblk; b0 += NB * kBlock) {
+      CoordBlock<EC, PT * DIM> cb[NB];
+      size_t s0[NB];
+      uint32_t hs[NB];
+      int bl[NB];
+      bool bv[NB];
+#pragma unroll
+      for (int k = 0; k < NB; ++k) {
+        const uint32_t j = b0 + (uint32_t)(k * kBlock) + threadIdx.x;
+        bv[k] = j < nblk;
+        const uint32_t s = (bv[k] ? j : 0u) * (uint32_t)PT;
+        const uint32_t wi = fdiv(s, pl.div_lp);
+        bl[k] = (int)((s - wi * (uint32_t)LP) / (uint32_t)PT);
+        const BinUnit bu = bin_unit(pl, g, w, wi);
+        s0[k] = bu.bqh * LP + (size_t)bl[k] * PT;
+        hs[k] = bu.hsub;
+        if (bv[k]) load_block<EC, PT * DIM>(cb[k], static_cast<const TC*>(bf.loc) + s0[k] * DIM);
+      }
+#pragma unroll
+      for (int k = 0; k < NB; ++k) {
+        if (!bv[k]) continue;
+        const BwdLevel lv = level_at(geo, bl[k]);
+#pragma unroll
+        for (int p = 0; p < PT; ++p) {
+          float xyz[DIM];
+#pragma unroll
+          for (int d = 0; d < DIM; ++d) xyz[d] = block_elem(cb[k], p * DIM + d);
+          count(lv, xyz, hs[k], s0[k] + p);
+        }
+      }
+    }
+  } else {
+    const uint32_t n = units * (uint32_t)LP;
+    for (uint32_t r0 = 0; r0 < n; r0 += NB * kBlock) {
+      float xyz[NB][DIM];
+      size_t si[NB];
+      uint32_t hs[NB];
+      int sl[NB];
+      bool sv[NB];
+#pragma unroll
+      for (int k = 0; k < NB; ++k) {
+        const uint32_t j = r0 + (uint32_t)(k * kBlock) + threadIdx.x;
+        sv[k] = j < n;
+        const uint32_t s = sv[k] ? j : 0u;
+        const uint32_t wi = fdiv(s, pl.div_lp);
+        const uint32_t r = s - wi * (uint32_t)LP;
+        sl[k] = (int)fdiv(r, pl.div_p);
+        const BinUnit bu = bin_unit(pl, g, w, wi);
+        si[k] = bu.bqh * LP + r;
+        hs[k] = bu.hsub;
+        const TC* lp = static_cast<const TC*>(bf.loc) + si[k] * DIM;
+#pragma unroll
+        for (int d = 0; d < DIM; ++d) xyz[k][d] = sv[k] ? (float)lp[d] : 0.0f;
+      }
+#pragma unroll
+      for (int k = 0; k < NB; ++k)
+        if (sv[k]) count(level_at(geo, sl[k]), xyz[k], hs[k], si[k]);
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < bins; i += kBlock)
+    bf.counts[((size_t)g * bins + i) * pl.wgpg + w] = s_hist[i];
+}
+
 // Atomic path: clear the n fp32 sums (16-byte aligned) before the scatter.
 __global__ __launch_bounds__(kBlock) void bwd_clear_sums_kernel(const BwdPlan pl, const BwdBuffers bf,
                                                                 uint32_t n) {
@@ -492,8 +606,8 @@ __global__ __launch_bounds__(kBlock) void bwd_clear_sums_kernel(const BwdPlan pl
 // Atomic path: round the fp32 sums to the value dtype, VEC elements per thread and step
 // (n is a multiple of VEC: C is). Invalid device shapes: every gradient becomes NaN
 // (n_loc grad_loc elements and n_attn = n_loc / DIM grad_attn elements in the coord dtype).
-// The sums follow the layout the sample-gradient kernel gathered from: (Bc, H, K, C) for
-// head-major plans, whose element (b, k, h, c) of grad_value is read across that transpose.
+// The sums follow the layout of value: (Bc, H, K, C) when value is head-major, whose element
+// (b, k, h, c) of grad_value is read across that transpose.
 template <typename EV, typename EC, int VEC>
 __global__ __launch_bounds__(kBlock) void bwd_round_kernel(const BwdPlan pl, const BwdBuffers bf,
                                                            uint32_t n, uint64_t n_loc, int dim) {
@@ -630,7 +744,7 @@ __global__ __launch_bounds__(kPlanThreads) void bwd_plan_kernel(const BwdPlan pl
 }
 
 // ------------------------------------------------------------------ 4: fill
-// Same workgroup -> units mapping as the sample-gradient kernel. In rounds of at most
+// Same workgroup -> units mapping as the count kernel. In rounds of at most
 // kFillStage samples (PT > 0: the workgroup's samples in memory order over all levels;
 // otherwise level by level): rank each sample within its bin (LDS atomics), scan the
 // round's per-bin counts, place the records in LDS sorted by bin, and copy them out so that
@@ -854,6 +968,14 @@ __device__ inline void lds_f32(const char* p, float (&v)[N]) {
   }
 }
 
+// N staged elements of type E from LDS, widened to fp32 (one 8-byte read for four 16-bit
+// elements, one 16-byte read for four fp32 ones).
+template <typename E, int N>
+__device__ inline void lds_elems(const char* p, float (&v)[N]) {
+  if constexpr (E::kBytes == 4) lds_f32<N>(p, v);
+  else widen<E, N>(*reinterpret_cast<const RawVec<N * 2>*>(p), v);
+}
+
 // Exclusive scan, in place, of the n + 1 counters c[0..n] of a region by one wave (c[n] is
 // zero before, the total after). c is 16-byte aligned and padded to a multiple of four
 // counters; each lane scans a run of whole quads (one 16-byte read and write each; a
@@ -886,17 +1008,20 @@ __device__ inline void wave_scan_counts(uint32_t* c, int n) {
 
 // One workgroup (kTileThreads<DIM> threads) per chunk of a tile's records, in sub-batches of
 // S <= kTileThreads<DIM> records; thread t owns record t of the sub-batch in registers. LDS
-// holds the sub-batch's grad_out rows widened to fp32, its (attn * corner weight, row
-// byte offset) entries sorted by region cell, and two sets of per-cell counters (one
-// being filled while the other is cleared). Per sub-batch, four barriers:
+// holds the value rows of the tile's region (staged once per chunk), the sub-batch's
+// grad_out rows in the value dtype, its (attn * corner weight, row byte offset) entries
+// sorted by region cell, and two sets of per-cell counters (one being filled while the
+// other is cleared). Per sub-batch, four barriers:
 //   1. every wave stages the grad_out rows of its 64 records (four lanes per 16-byte
 //      chunk group, the row index handed over with ds_bpermute) while each record's
 //      owner counts its corners per region cell (LDS integer atomics give the ranks);
-//   2. one wave scans the counters; the other counter set is cleared;
+//   2. one wave scans the counters; the other counter set is cleared; each owner forms
+//      its record's corner dot products <grad_out, v_c> from LDS and stores the sample's
+//      grad_attn and clamp-masked grad_loc;
 //   3. owners place their entries at offset + rank and fetch the next sub-batch's record;
 //   4. the thread owning (region cell, channel chunk) sums its cell's entries into fp32
 //      registers.
-template <int DIM, typename EV, typename EC, int VEC>
+template <int DIM, typename EV, typename EC, int VEC, bool DOTS>
 __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile_kernel(const BwdPlan pl,
                                                                 const BwdBuffers bf) {
   constexpr int NT = kTileThreads<DIM>;
@@ -908,6 +1033,7 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
                                            // lanes of one cell read a staged row conflict-free
   constexpr int GB = 4;                   // grad_out chunk loads in flight per thread
   typedef typename EV::T TV;
+  typedef typename EC::T TC;
   extern __shared__ __attribute__((aligned(16))) char s_mem[];
 
   // Chunks are dealt to XCDs in contiguous ranges (workgroup i runs on XCD i % xcds), so the
@@ -941,12 +1067,19 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
   const TileCoord tc = decode_tile(pl, geo, t, &lv);
 
   const uint32_t S = pl.S;
-  const uint32_t grow = (uint32_t)pl.C * 4u;  // bytes of one staged fp32 grad_out row
-  char* s_g = s_mem;                                                   // [S][C] fp32
+  // bytes between staged grad_out rows (value dtype, C * s rounded up to an odd number of
+  // 16-byte slots, so the same chunk of consecutive records' rows falls in different banks)
+  const uint32_t grow = pl.grow;
+  // bytes between staged value rows: an odd number of 16-byte slots, so the same chunk of
+  // random rows falls in every slot of a bank row, not in every second or fourth one
+  const uint32_t vrow = pl.vrow;
+  char* s_g = s_mem;                                                   // [S][grow] grad_out
   uint2* s_ent = reinterpret_cast<uint2*>(s_g + pl.lds_g_bytes);       // [S * NC]
   // two counter sets of rcells + 1 counters, each padded to whole quads (16-byte aligned:
-  // S * C * 4 and S * NC * 8 are multiples of 16)
+  // S * grow and S * NC * 8 are multiples of 16)
   uint32_t* s_cnt2 = reinterpret_cast<uint32_t*>(s_ent + (size_t)S * NC);
+  const int ncp = (pl.rcells + 4) & ~3;  // counter-set stride, sized for a full region
+  char* s_v = reinterpret_cast<char*>(s_cnt2 + 2 * ncp);  // [region cells][vrow] value rows
   // compact region: the owner items and counters cover only its cells (a partial tile on a
   // coarse level's edge spreads its entries over all owner threads instead of the few whose
   // fixed-layout cells it touches: C2 level-3 edge chunks 176 -> 110 us, tile kernel 174 -> 161 us)
@@ -958,6 +1091,23 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
   const TV* gout = static_cast<const TV*>(bf.grad_out) + ((size_t)tc.b * pl.Q * pl.H + tc.h) * pl.C;
   const size_t grad_q_stride = (size_t)pl.H * pl.C;  // elements between queries of grad_out
 
+  // the region's value rows -> LDS, once per chunk: every corner of the chunk's samples
+  // (their <grad_out, v_c> dot products give grad_attn and grad_loc)
+  if constexpr (DOTS) {
+    const TV* val = static_cast<const TV*>(bf.value);
+    const int exy = rg.ex * rg.ey;
+    for (int i = tid; i < ncell_r * (int)nvec; i += NT) {
+      const int cell = (int)fdiv((uint32_t)i, pl.div_nvec), ch = i - cell * (int)nvec;
+      const int rz = cell / exy, rxy = cell - rz * exy;
+      const int ry = rxy / rg.ex, rx = rxy - ry * rg.ex;
+      const uint32_t row = (uint32_t)lv.start + ((uint32_t)(tc.Z0 + rz) * lv.H + (tc.Y0 + ry)) * lv.W +
+                           (tc.X0 + rx);
+      const size_t e = pl.head_major ? (((size_t)tc.b * pl.H + tc.h) * pl.K + row) * pl.C
+                                     : (((size_t)tc.b * pl.K + row) * pl.H + tc.h) * pl.C;
+      *reinterpret_cast<RawVec<VB>*>(s_v + cell * vrow + ch * VB) = glb_load<VB>(val + e + ch * VEC);
+    }
+  }
+
   const int onv = pl.onv;
   float acc[MI][OV];
 #pragma unroll
@@ -965,7 +1115,6 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
 #pragma unroll
     for (int k = 0; k < OV; ++k) acc[m][k] = 0.0f;
 
-  const int ncp = (pl.rcells + 4) & ~3;  // counter-set stride, sized for a full region
   for (int i = tid; i < 2 * ncp; i += NT) s_cnt2[i] = 0u;
   uint32_t rec[RW];
 #pragma unroll
@@ -1000,7 +1149,7 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
           const uint32_t r = (uint32_t)wv * kWave + lr;
           if (r < nrec) {
             gr[k] = glb_load<VB>(gout + (size_t)qq * grad_q_stride + ch * VEC);
-            dst[k] = r * grow + ch * (VEC * 4u);
+            dst[k] = r * grow + ch * (uint32_t)VB;
           }
         }
       }
@@ -1016,28 +1165,91 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
         }
       }
 #pragma unroll
-      for (int k = 0; k < GB; ++k) {
-        if (dst[k] == 0xffffffffu) continue;
-        float v[VEC];
-        widen<EV, VEC>(gr[k], v);
-        float* d = reinterpret_cast<float*>(s_g + dst[k]);
-        if constexpr (VEC % 4 == 0) {
-#pragma unroll
-          for (int i = 0; i < VEC; i += 4)
-            *reinterpret_cast<float4*>(d + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
-        } else {
-#pragma unroll
-          for (int i = 0; i < VEC; ++i) d[i] = v[i];
-        }
-      }
+      for (int k = 0; k < GB; ++k)
+        if (dst[k] != 0xffffffffu) *reinterpret_cast<RawVec<VB>*>(s_g + dst[k]) = gr[k];
     }
     lds_sync();
 
-    // 2. scan this set of counters; clear the other (last read in the previous sub-batch)
+    // 2. scan this set of counters; clear the other (last read in the previous sub-batch);
+    // each owner forms its record's corner dot products from the staged grad_out row and
+    // region rows and stores the sample's grad_attn and clamp-masked grad_loc
     if (wv == 0) wave_scan_counts(s_cnt, ncell_r);
     {
       uint32_t* o = s_cnt2 + (par ^ 1) * ncp;
       for (int i = tid; i <= ncell_r; i += NT) o[i] = 0u;
+    }
+    if (DOTS && has) {
+      uint32_t vo[NC];
+      float dot[NC];
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc) {
+        vo[cc] = slot[cc] != 0xffffffffu ? (slot[cc] >> 16) * vrow : 0u;
+        dot[cc] = 0.0f;
+      }
+      const char* gp = s_g + (uint32_t)tid * grow;
+      for (uint32_t j = 0; j < nvec; ++j) {
+        const RawVec<VB> gk = *reinterpret_cast<const RawVec<VB>*>(gp + j * VB);
+        if constexpr (EV::kBytes == 2 && VEC >= 2) {
+          // 16-bit grad_out and value: each pair of channels is one dot2 of the raw dwords
+          // (exact products, fp32 sum)
+#pragma unroll
+          for (int cc = 0; cc < NC; ++cc) {
+            const RawVec<VB> r = *reinterpret_cast<const RawVec<VB>*>(s_v + vo[cc] + j * VB);
+#pragma unroll
+            for (int e = 0; e < VEC / 2; ++e) dot[cc] = dot2_acc<EV>(raw_dword(r, e), raw_dword(gk, e), dot[cc]);
+          }
+        } else {
+          float g[VEC];
+          widen<EV, VEC>(gk, g);
+#pragma unroll
+          for (int cc = 0; cc < NC; ++cc) {
+            float v[VEC];
+            widen<EV, VEC>(*reinterpret_cast<const RawVec<VB>*>(s_v + vo[cc] + j * VB), v);
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) dot[cc] = __builtin_fmaf(g[e], v[e], dot[cc]);
+          }
+        }
+      }
+      // corners outside the level or the region read zero (the zero padding)
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc)
+        if (slot[cc] == 0xffffffffu) dot[cc] = 0.0f;
+      float s_attn, s_x, s_y, s_z;
+      corner_grads<DIM>(sm, dot, s_attn, s_x, s_y, s_z);
+      const float a = as_float(rec[RW - 1]);
+      const uint32_t p = (rec[0] & kRecIdMask) - q * (uint32_t)pl.P;
+      const size_t si = (((size_t)tc.b * pl.Q + q) * pl.H + tc.h) * (size_t)(pl.L * pl.P) +
+                        (size_t)tc.l * pl.P + p;
+      TC* gl = static_cast<TC*>(bf.grad_loc) + si * DIM;
+      static_cast<TC*>(bf.grad_attn)[si] = (TC)s_attn;
+      float o[DIM];
+      o[0] = sm.ax.pass ? (a * s_x) * (float)lv.W : 0.0f;
+      o[1] = sm.ay.pass ? (a * s_y) * (float)lv.H : 0.0f;
+      if constexpr (DIM == 3) o[2] = sm.az.pass ? (a * s_z) * (float)lv.D : 0.0f;
+      // scattered stores cost a request each: the 2D pair as one store where aligned
+      if constexpr (DIM == 2) {
+        if (pl.coords_aligned) {
+          store_block<EC, 2>(gl, o);
+        } else {
+          gl[0] = (TC)o[0];
+          gl[1] = (TC)o[1];
+        }
+      } else if constexpr (EC::kBytes == 2) {
+        // three 16-bit values: the 4-byte-aligned pair as one store
+        if (pl.coords_aligned && (si & 1u) == 0u) {
+          *reinterpret_cast<uint32_t*>(gl) = pack2<EC>(o[0], o[1]);
+          gl[2] = (TC)o[2];
+        } else if (pl.coords_aligned) {
+          gl[0] = (TC)o[0];
+          *reinterpret_cast<uint32_t*>(gl + 1) = pack2<EC>(o[1], o[2]);
+        } else {
+#pragma unroll
+          for (int d = 0; d < DIM; ++d) gl[d] = (TC)o[d];
+        }
+      } else {
+#pragma unroll
+        for (int d = 0; d < DIM; ++d) gl[d] = (TC)o[d];
+      }
     }
     lds_sync();
 
@@ -1083,7 +1295,7 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
       const int it = tid + m * NT;
       if (it >= ncell_r * onv) continue;
       const int ce = (int)fdiv((uint32_t)it, pl.div_onv), ch = it - ce * onv;
-      const char* gb = s_g + ch * (OV * 4);
+      const char* gb = s_g + ch * (OV * EV::kBytes);
       uint32_t e = eb[m];
       const uint32_t e1 = ee[m];
       for (; e + 4 <= e1; e += 4) {
@@ -1092,7 +1304,7 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
         for (int j = 0; j < 4; ++j) en[j] = s_ent[e + j];
         float gv[4][OV];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) lds_f32<OV>(gb + en[j].y, gv[j]);
+        for (int j = 0; j < 4; ++j) lds_elems<EV, OV>(gb + en[j].y, gv[j]);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -1104,9 +1316,9 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
         const uint2 t1 = s_ent[r > 1 ? e + 1 : e];
         const uint2 t2 = s_ent[r > 2 ? e + 2 : e];
         float g0[OV], g1[OV], g2[OV];
-        lds_f32<OV>(gb + t0.y, g0);
-        lds_f32<OV>(gb + t1.y, g1);
-        lds_f32<OV>(gb + t2.y, g2);
+        lds_elems<EV, OV>(gb + t0.y, g0);
+        lds_elems<EV, OV>(gb + t1.y, g1);
+        lds_elems<EV, OV>(gb + t2.y, g2);
         const float w1 = r > 1 ? as_float(t1.x) : 0.0f, w2 = r > 2 ? as_float(t2.x) : 0.0f;
 #pragma unroll
         for (int k = 0; k < OV; ++k) {
@@ -1270,7 +1482,8 @@ hipError_t run_bwd_t(const BwdPlan& pl, const BwdGeom* host_geom, const GeomArgs
   const size_t hist_bytes = (size_t)pl.bins_cap * sizeof(uint32_t);
   if (nbin_wg == 0) return hipErrorInvalidValue;
   BwdGeom* geom = const_cast<BwdGeom*>(bf.geom);
-  // host shapes: the sample-gradient kernel gets the geometry as an argument and stores it
+  // host shapes: the first kernel (count, or the atomic kernel) gets the geometry as an
+  // argument and stores it
   BwdPlan plx = pl;
   plx.geom_arg = host_geom ? 1 : 0;
   static const BwdGeom kNoGeom{};
@@ -1296,28 +1509,43 @@ hipError_t run_bwd_t(const BwdPlan& pl, const BwdGeom* host_geom, const GeomArgs
                        pl.grad_loc_elems, DIM);
     if (pl.static_atomic) return hipGetLastError();
   }
-  // compile-time lane-group size for the common 16-byte lane loads of 4 or 8 lanes per unit
-  if (pl.P == 4 && pl.coords_aligned && pl.lpu_log2 == 2)
-    hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 4, 2>), dim3(nbin_wg), dim3(kGradThreads),
-                       hist_bytes, s, plx, bf, hg);
-  else if (pl.P == 4 && pl.coords_aligned && pl.lpu_log2 == 3)
-    hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 4, 3>), dim3(nbin_wg), dim3(kGradThreads),
-                       hist_bytes, s, plx, bf, hg);
-  else if (pl.P == 8 && pl.coords_aligned && pl.lpu_log2 == 2)
-    hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 8, 2>), dim3(nbin_wg), dim3(kGradThreads),
-                       hist_bytes, s, plx, bf, hg);
-  else if (pl.P == 8 && pl.coords_aligned && pl.lpu_log2 == 3)
-    hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 8, 3>), dim3(nbin_wg), dim3(kGradThreads),
-                       hist_bytes, s, plx, bf, hg);
-  else if (pl.P == 4 && pl.coords_aligned)
-    hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 4, -1>), dim3(nbin_wg), dim3(kGradThreads),
-                       hist_bytes, s, plx, bf, hg);
-  else if (pl.P == 8 && pl.coords_aligned)
-    hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 8, -1>), dim3(nbin_wg), dim3(kGradThreads),
-                       hist_bytes, s, plx, bf, hg);
-  else
-    hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 0, -1>), dim3(nbin_wg), dim3(kGradThreads),
-                       hist_bytes, s, plx, bf, hg);
+  // the plan's tile_dots is set exactly for 16-bit values
+  constexpr bool kDots = EV::kBytes == 2;
+  if (pl.tile_dots != (kDots ? 1 : 0)) return hipErrorInvalidValue;
+  if constexpr (kDots) {
+    // binned plans, 16-bit values: per-(tile, workgroup) sample counts from the coordinates
+    // alone (the tile kernel forms the sample gradients)
+    if (pl.P == 4 && pl.coords_aligned)
+      hipLaunchKernelGGL((bwd_count_kernel<DIM, EC, 4>), dim3(nbin_wg), dim3(kBlock), hist_bytes, s, plx, bf, hg);
+    else if (pl.P == 8 && pl.coords_aligned)
+      hipLaunchKernelGGL((bwd_count_kernel<DIM, EC, 8>), dim3(nbin_wg), dim3(kBlock), hist_bytes, s, plx, bf, hg);
+    else
+      hipLaunchKernelGGL((bwd_count_kernel<DIM, EC, 0>), dim3(nbin_wg), dim3(kBlock), hist_bytes, s, plx, bf, hg);
+  } else {
+    // binned plans, fp32 values: sample gradients gathered per unit, with the counts
+    // compile-time lane-group size for the common 16-byte lane loads of 4 or 8 lanes per unit
+    if (pl.P == 4 && pl.coords_aligned && pl.lpu_log2 == 2)
+      hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 4, 2>), dim3(nbin_wg), dim3(kGradThreads),
+                         hist_bytes, s, plx, bf, hg);
+    else if (pl.P == 4 && pl.coords_aligned && pl.lpu_log2 == 3)
+      hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 4, 3>), dim3(nbin_wg), dim3(kGradThreads),
+                         hist_bytes, s, plx, bf, hg);
+    else if (pl.P == 8 && pl.coords_aligned && pl.lpu_log2 == 2)
+      hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 8, 2>), dim3(nbin_wg), dim3(kGradThreads),
+                         hist_bytes, s, plx, bf, hg);
+    else if (pl.P == 8 && pl.coords_aligned && pl.lpu_log2 == 3)
+      hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 8, 3>), dim3(nbin_wg), dim3(kGradThreads),
+                         hist_bytes, s, plx, bf, hg);
+    else if (pl.P == 4 && pl.coords_aligned)
+      hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 4, -1>), dim3(nbin_wg), dim3(kGradThreads),
+                         hist_bytes, s, plx, bf, hg);
+    else if (pl.P == 8 && pl.coords_aligned)
+      hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 8, -1>), dim3(nbin_wg), dim3(kGradThreads),
+                         hist_bytes, s, plx, bf, hg);
+    else
+      hipLaunchKernelGGL((bwd_grad_kernel<DIM, EV, EC, VEC, 0, -1>), dim3(nbin_wg), dim3(kGradThreads),
+                         hist_bytes, s, plx, bf, hg);
+  }
   if (pl.T_cap == 0) return hipGetLastError();  // no cell in any level: grad_value is empty
   // grids sized by T_cap (the launch's tiles when the host knows the shapes, an upper bound
   // otherwise); workgroups beyond the geometry's T exit
@@ -1334,7 +1562,7 @@ hipError_t run_bwd_t(const BwdPlan& pl, const BwdGeom* host_geom, const GeomArgs
     hipLaunchKernelGGL((bwd_fill_kernel<DIM, EC, 8>), dim3(nbin_wg), dim3(kBlock), fill_bytes, s, pl, bf);
   else
     hipLaunchKernelGGL((bwd_fill_kernel<DIM, EC, 0>), dim3(nbin_wg), dim3(kBlock), fill_bytes, s, pl, bf);
-  hipLaunchKernelGGL((bwd_tile_kernel<DIM, EV, EC, VEC>), dim3(pl.grid_chunks),
+  hipLaunchKernelGGL((bwd_tile_kernel<DIM, EV, EC, VEC, kDots>), dim3(pl.grid_chunks),
                      dim3(kTileThreads<DIM>), pl.lds_bytes, s, pl, bf);
   hipLaunchKernelGGL((bwd_fold_kernel<DIM, EV, VEC>), dim3(pl.T_cap), dim3(kBlock), 0, s, pl, bf);
   return hipGetLastError();
@@ -1411,12 +1639,11 @@ BwdSizes bwd_sizes(const BwdPlan& pl, uint64_t samples, int dim) {
   // atomic path: one fp32 sum per grad_value element of a launch (groups << hg_log2 =
   // batches * H)
   z.sum_floats = sums ? ((uint64_t)pl.groups << pl.hg_log2) * (uint64_t)pl.K * pl.C : 0u;
-  z.value_h_bytes = pl.head_major && !pl.hm_given ? (uint64_t)pl.value_bytes : 0u;
   z.geom_bytes = sizeof(BwdGeom);
   auto al = [](uint64_t b) { return (b + 255) & ~(uint64_t)255; };
   z.total_bytes = al(z.counts * 4) + al(z.tile_n * 4) + al(z.bin_start * 4) + al(z.chunk_off * 4) +
                   al(z.chunk_tile * 4) + al(z.record_words * 4) + al(z.scratch_floats * 4) +
-                  al(z.sum_floats * 4) + al(z.value_h_bytes) + al(z.geom_bytes);
+                  al(z.sum_floats * 4) + al(z.geom_bytes);
   return z;
 }
 

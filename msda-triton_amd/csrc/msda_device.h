@@ -181,6 +181,21 @@ __device__ inline float dot2_acc(uint32_t a, uint32_t b, float acc) {
   }
 }
 
+// Two fp32 values packed into one dword of 16-bit elements (a in the low half), rounded to
+// nearest even; exact for values that are representable in the 16-bit type.
+template <typename E>
+__device__ inline uint32_t pack2(float a, float b) {
+  if constexpr (__is_same(E, BF16)) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    const bf2 v = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, v);
+  } else {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 v = {(_Float16)a, (_Float16)b};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+}
+
 // fp32 -> storage type, round to nearest even (hardware conversions on gfx950).
 template <typename E>
 __device__ inline typename E::T narrow(float x) {

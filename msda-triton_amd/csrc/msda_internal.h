@@ -21,11 +21,10 @@ constexpr int kTileMaxItems = 5;
 constexpr int tile_owner_vec(int vec) { return vec < 4 ? vec : 4; }
 constexpr int kTileWavesPerSimd = 4;  // tile-kernel occupancy target (128 VGPRs)
 constexpr int kFillStage = 2048;      // records staged in LDS per fill round
-constexpr int kGradThreads = 256;     // threads of the backward sample-gradient kernel
-// unit groups each thread of the sample-gradient and fill kernels handles in turn. 3D
-// launches that keep at least kGradWgsPerCu workgroups per CU at twice as many rounds use
-// 2 * kGradRounds (C5 sample gradients 476 -> 464 us, fill 113 -> 110 us); 2D keeps
-// kGradRounds (C2: 114 us against 127 us at 8 rounds)
+constexpr int kGradThreads = 256;     // threads of the backward count, fill and atomic kernels
+// units (b, q, h) of a count / fill workgroup: kGradRounds unit groups of 2^lpu_log2 lanes per
+// thread. 3D launches that keep at least kGradWgsPerCu workgroups per CU at twice as many
+// rounds use 2 * kGradRounds (C5 fill 113 -> 110 us)
 constexpr int kGradRounds = 4;
 constexpr int kGradWgsPerCu = 2;
 // threads of the staged forward kernel: 12 waves per CU leave each lane 168 VGPRs, so
@@ -118,7 +117,7 @@ struct BwdLevel {
 // Level geometry of one backward launch: what depends on the level shapes. It lives in
 // the workspace and the kernels read it through a constant-address-space pointer, so a
 // wave-uniform field is one scalar load, as a kernel argument would be. Host-resident
-// shapes: computed on the host and passed to the sample-gradient kernel, which stores it.
+// shapes: computed on the host and passed to the first kernel, which stores it.
 // Device-resident shapes: computed by bwd_geom_kernel from the shapes on the device, so the
 // host never reads them (no device-to-host copy, no synchronisation; the launch sequence
 // can be graph-captured).
@@ -227,20 +226,30 @@ struct BwdPlan {
   int32_t lpu_log2, nvec;
   int32_t clamp;
   int32_t coords_aligned;      // loc and attn are 16-byte aligned: per-batch block loads allowed
-  int32_t head_major;          // the sample-gradient kernel reads BwdBuffers::value_h
-  int32_t hm_given;            // value_h is the caller's head-major value (no relayout, no
-                               // workspace for it)
+  int32_t head_major;          // value is the caller's head-major (B, H, K, C) copy
+                               // (MSDA_FLAG_VALUE_HEAD_MAJOR): the tile kernel's region rows,
+                               // the atomic path's gathers and its fp32 sums follow that layout
   int32_t static_atomic;       // the host chose the atomic path (levels beyond the LDS binning,
                                // or sample ids beyond a record): grad_value is scattered with
                                // fp32 atomics into BwdBuffers::sums, then rounded into grad_value
   int32_t fallback;            // device shapes: the binned and the atomic kernels are both
                                // launched and each exits unless BwdGeom::atomic selects it
-  int32_t geom_arg;            // host shapes: the sample-gradient kernel (the first to need the
-                               // geometry) reads it from its kernel argument and stores it in
+  int32_t geom_arg;            // host shapes: the first kernel (count, or the atomic kernel)
+                               // reads the geometry from its kernel argument and stores it in
                                // the workspace for the kernels after it
   float lo_g, hi_g;
   uint32_t value_bytes;
-  uint32_t lds_g_bytes;        // bytes of the staged fp32 grad_out rows of a sub-batch
+  int32_t tile_dots;           // 16-bit values: the tile kernel forms grad_loc / grad_attn from
+                               // its staged region rows and a count kernel bins the samples;
+                               // else (fp32) the sample-gradient kernel gathers the corner rows
+                               // per unit and bins the samples (fp32 rows leave too little LDS
+                               // for the region: C2 fp32 backward 430 against 537 us)
+  uint32_t grow;               // bytes between the tile kernel's staged grad_out rows (value
+                               // dtype; with tile_dots C * s rounded up to an odd number of
+                               // 16-byte slots)
+  uint32_t vrow;               // bytes between the tile kernel's staged value rows (C * s
+                               // rounded up to an odd number of 16-byte slots)
+  uint32_t lds_g_bytes;        // bytes of the staged grad_out rows of a sub-batch
   uint32_t lds_bytes;          // total dynamic LDS of the tile kernel
   uint32_t max_chunks;         // upper bound of the chunk count
   uint32_t grid_chunks;        // tile-kernel grid: max_chunks rounded up to a multiple of xcds
@@ -250,7 +259,6 @@ struct BwdPlan {
 
 struct BwdBuffers {
   const void* value;
-  const void* value_h;   // head-major copy of value (B, H, K, C) when the plan says so
   const void* loc;
   const void* attn;
   const void* grad_out;
@@ -270,7 +278,6 @@ struct BwdBuffers {
 
 struct BwdSizes {
   uint64_t counts, tile_n, bin_start, chunk_off, chunk_tile, record_words, scratch_floats, sum_floats;
-  uint64_t value_h_bytes;  // head-major value copy (0 when the plan does not use one)
   uint64_t geom_bytes;
   uint64_t total_bytes;
 };

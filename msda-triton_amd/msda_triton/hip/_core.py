@@ -288,8 +288,8 @@ def backward(dim: int, grad_output: torch.Tensor, value_c: torch.Tensor, levels:
              loc_c: torch.Tensor, attn_c: torch.Tensor, clamp_grid: bool, clamp_eps: float,
              value_hm: torch.Tensor | None = None):
     """Launch msda_bwd. Returns (grad_value, grad_loc, grad_attn) in the kernel dtypes,
-    all freshly allocated and contiguous. value_hm: the forward's head-major copy of value_c
-    (then the backward gathers from it and makes no copy of its own)."""
+    all freshly allocated and contiguous. value_hm: a head-major (B, H, K, C) copy of value_c,
+    such as the forward's workspace, passed instead of value_c (MSDA_FLAG_VALUE_HEAD_MAJOR)."""
     lib = _lib.load()
     grad_out = _aligned(grad_output.to(dtype=value_c.dtype).contiguous())
     value_c = _aligned(value_c)
@@ -328,12 +328,11 @@ def fn_forward(ctx, name: str, dim: int, value, value_spatial_shapes, sampling_l
     """Body of MSDA2DFn.forward / MSDA3DFn.forward (reference triton/msda_2d.py:749-775)."""
     validate_inputs(name, dim, value, value_spatial_shapes, sampling_locations, attention_weights)
     levels = prepare_levels(dim, value, value_spatial_shapes)
-    out, value_c, loc_c, attn_c, value_hm = forward(dim, value, levels, sampling_locations,
-                                                    attention_weights, clamp_grid, clamp_eps)
+    # the forward's head-major copy of value (its workspace) is not kept: the backward reads
+    # value rows once per tile region, in either layout
+    out, value_c, loc_c, attn_c, _ = forward(dim, value, levels, sampling_locations,
+                                             attention_weights, clamp_grid, clamp_eps)
     ctx.save_for_backward(value_c, loc_c, attn_c)
-    # the head-major copy the forward gathered from serves the backward too (one relayout
-    # per training step instead of two); a workspace, not an input or output of the op
-    ctx.value_hm = value_hm if any(ctx.needs_input_grad) else None
     ctx.levels = levels
     ctx.clamp_grid = clamp_grid
     ctx.clamp_eps = clamp_eps
@@ -346,8 +345,7 @@ def fn_backward(ctx, dim: int, grad_output: torch.Tensor):
     returns (grad_value, None, grad_loc, grad_attn, None, None) in the input dtypes."""
     value_c, loc_c, attn_c = ctx.saved_tensors
     gv, gl, ga = backward(dim, grad_output, value_c, ctx.levels, loc_c, attn_c,
-                          ctx.clamp_grid, ctx.clamp_eps, ctx.value_hm)
-    ctx.value_hm = None
+                          ctx.clamp_grid, ctx.clamp_eps)
     vdt, ldt, adt = ctx.in_dtypes
     return gv.to(vdt), None, gl.to(ldt), ga.to(adt), None, None
 

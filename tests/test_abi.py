@@ -120,12 +120,12 @@ def test_bwd_workspace_bytes_host_only():
     s3 = (32, 64, 64, 16, 32, 32, 8, 16, 16, 4, 8, 8)
     n3 = lib.msda_bwd_workspace_bytes(ctypes.byref(d3), _shapes(s3))
     assert n3 > 0
-    # a caller-supplied head-major value (the forward's copy): the relayout's workspace,
-    # the whole value (149760 * 8 * 32 bf16), is no longer needed
+    # the backward reads value rows only per tile region, so it never relays value out: a
+    # caller-supplied head-major value (the forward's copy) needs the same workspace
     h3 = _desc(dim=3, batch=1, num_keys=149760, num_queries=32768, num_points=8,
                flags=_lib.FLAG_VALUE_HEAD_MAJOR)
     assert lib.msda_fwd_workspace_bytes(ctypes.byref(d3)) == 149760 * 8 * 32 * 2
-    assert n3 - lib.msda_bwd_workspace_bytes(ctypes.byref(h3), _shapes(s3)) == 149760 * 8 * 32 * 2
+    assert lib.msda_bwd_workspace_bytes(ctypes.byref(h3), _shapes(s3)) == n3
 
 
 def test_bwd_levels_beyond_binning_plan_atomic_path():
