@@ -49,8 +49,8 @@ HBM_PEAK_GBPS = 8000.0
 # kernels behind the roofline objects (the C2 bf16 launch: 2D, bf16 value and coordinates,
 # 8 channels per lane, 4 points per coordinate block, quad-shared geometry)
 FWD_KERNEL = "msda::msda_fwd_staged_kernel<2, msda::BF16, msda::BF16, 8, 4, true, false>"
-BWD_KERNELS = ("msda_bwd entry: bwd_grad_kernel, bwd_colscan_kernel, bwd_plan_kernel, "
-               "bwd_fill_kernel, bwd_tile_kernel, bwd_fold_kernel and workspace clears")
+BWD_KERNELS = ("msda_bwd entry (16-bit values): bwd_count_kernel, bwd_colscan_kernel, "
+               "bwd_plan_kernel, bwd_fill_kernel, bwd_tile_kernel, bwd_fold_kernel")
 
 CONFIGS = {
     "c1": dict(dim=2, B=1, H=8, C=32, shapes=[(32, 32), (16, 16)], Q=100, P=4, dtype="fp32",
