@@ -266,7 +266,7 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
   const bool ids_fit = (uint64_t)d->num_queries * d->num_points <= (uint64_t)msda::kRecIdMask;
   // Tile extents and sub-batch size: start from 16x16 (2D) / 8x8x8 (3D) cells and
   // S = kTileThreads<dim> records (one per thread); halve the largest tile extent until a thread
-  // owns at most kTileMaxItems (region cell, owner chunk) items, and lower S in steps of
+  // owns at most tile_max_items (region cell, owner chunk) items, and lower S in steps of
   // half a wave until the sub-batch's grad_out rows, sorted entries, two counter sets and the
   // region's value rows fit the LDS share of one workgroup. Fewer records per sub-batch cost
   // more than fewer workgroups per CU (C2 tile kernel: S = 160 at four workgroups per CU
@@ -282,7 +282,8 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
   const uint32_t grow = tile_dots ? ((uint32_t)(d->channels * s) + 15u) / 32u * 32u + 16u
                                   : (uint32_t)(d->channels * s);
   const uint32_t vrow = tile_dots ? grow : 0u;
-  const int onv = d->channels / msda::tile_owner_vec(lay.vec_bytes / s);
+  const int ov = msda::tile_owner_vec(lay.vec_bytes / s, s);
+  const int onv = d->channels / ov;
   int T[3];
   uint32_t S = NT, lds = 0;
   int rcells = 0;
@@ -302,7 +303,7 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
     for (;;) {
       const int rz = d->dim == 3 ? T[2] + 1 : 1;
       rcells = (T[0] + 1) * (T[1] + 1) * rz;
-      const int mi = d->dim == 2 ? msda::kTileMaxItems<2> : msda::kTileMaxItems<3>;
+      const int mi = msda::tile_max_items(ov);
       if ((uint64_t)rcells * onv > (uint64_t)mi * NT) {
         if (!shrink()) return false;
         continue;

@@ -1028,9 +1028,10 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
   constexpr int VB = VEC * EV::kBytes;
   constexpr int NC = 1 << DIM;
   constexpr int RW = DIM + 2;        // words per record
-  constexpr int MI = kTileMaxItems<DIM>;  // owner items per thread
-  constexpr int OV = tile_owner_vec(VEC);  // channels per owner item: 16 fp32 bytes, so the
-                                           // lanes of one cell read a staged row conflict-free
+  // channels per owner item: 16 staged bytes, so the lanes of one cell read a staged row
+  // conflict-free; owner items per thread
+  constexpr int OV = tile_owner_vec(VEC, EV::kBytes);
+  constexpr int MI = tile_max_items(OV);
   constexpr int GB = 4;                   // grad_out chunk loads in flight per thread
   typedef typename EV::T TV;
   typedef typename EC::T TC;

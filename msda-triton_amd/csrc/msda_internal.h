@@ -14,11 +14,12 @@ constexpr int kMaxLevels = 64;
 // double the bins and the fill's work)
 template <int DIM>
 constexpr int kTileThreads = DIM == 2 ? 256 : 512;
-// (region cell, 4-channel chunk) owner items per tile thread
-template <int DIM>
-constexpr int kTileMaxItems = 5;
-// channels per owner item of the tile kernel for VEC channels per value load
-constexpr int tile_owner_vec(int vec) { return vec < 4 ? vec : 4; }
+// channels per owner item of the tile kernel for VEC channels per value load and eb bytes
+// per staged element: 16 staged bytes, so the lanes of one cell read a staged row in one
+// conflict-free pass (four fp32 or eight 16-bit channels)
+constexpr int tile_owner_vec(int vec, int eb) { return vec < 16 / eb ? vec : 16 / eb; }
+// (region cell, channel chunk) owner items per tile thread: 20-24 fp32 accumulators
+constexpr int tile_max_items(int ov) { return ov >= 8 ? 3 : 5; }
 constexpr int kTileWavesPerSimd = 4;  // tile-kernel occupancy target (128 VGPRs)
 constexpr int kFillStage = 2048;      // records staged in LDS per fill round
 constexpr int kGradThreads = 256;     // threads of the backward count, fill and atomic kernels
@@ -209,7 +210,7 @@ struct BwdPlan {
   int32_t TX, TY, TZ;          // owned cells per tile, powers of two (TZ = 1 in 2D)
   int32_t tx_log2, ty_log2, tz_log2;
   FastDiv div_nvec;            // divisor nvec (value-load chunks per row)
-  int32_t onv;                 // owner chunks per row in the tile kernel: C / tile_owner_vec(VEC)
+  int32_t onv;                 // owner chunks per row in the tile kernel: C / tile_owner_vec(VEC, s)
   FastDiv div_onv;             // divisor onv (owner item -> cell, chunk)
   FastDiv div_tx, div_txy;     // divisors TX and TX * TY (owned cell -> lx, ly, lz)
   int32_t RX, RY, RZ;          // region: tile + 1 along each axis (RZ = 1 in 2D)
