@@ -236,6 +236,36 @@ class ParitySuite:
                               coord_f32=True)
         assert max_rel(gv.float(), bv) <= FWD_TOL_HALF and max_rel(ga.float(), ba) <= FWD_TOL_HALF
 
+    @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+    def test_half_precision_no_clamp_outside_levels(self, dtype) -> None:
+        """16-bit inputs without the grid clamp, locations over [-0.3, 1.3]: samples with no
+        corner inside their level get exactly zero grad_loc and grad_attn (in the binned
+        backward the count pass writes those, the tile kernel all others); every gradient
+        against the float64 oracle on the upcast inputs. The allocator's memory is filled
+        with NaN first, so a gradient left unwritten cannot pass."""
+        value, shapes, loc, attn = self.inputs(batch_size=2, num_queries=60, num_heads=4,
+                                               dim_per_head=32)
+        loc = loc * 1.6 - 0.3
+        value, loc, attn = (t.to(dtype) for t in (value, loc, attn))
+        g = torch.Generator().manual_seed(11)
+        grad_out = torch.randn(2, 60, 4 * 32, generator=g).to(dtype)
+        vf, lf, af, gf = (t.float() for t in (value, loc, attn, grad_out))
+        # samples whose pixel coordinate leaves [-1, size) on some axis have no corner inside
+        u = torch.from_numpy(brute.coords(shapes, lf, clamp_grid=False, coord_f32=True))
+        size = shapes.flip(-1).to(u.dtype).view(1, 1, 1, -1, 1, self.dim)
+        outside = ((u < -1) | (u >= size)).any(-1)
+        assert int(outside.sum()) > 100
+        poison = torch.full((1 << 22,), float("nan"), device=self.device)
+        del poison
+        out, gv, gl, ga = self.run_fwd_bwd(value, shapes, loc, attn, grad_out, clamp_grid=False)
+        ref = brute.fwd(vf, shapes, lf, af, clamp_grid=False, coord_f32=True)
+        assert max_rel(out.float(), ref) <= FWD_TOL_HALF
+        bv, bl, ba = brute.bwd(vf, shapes, lf, af, gf, False, 1e-4, coord_f32=True)
+        for name, got, want in (("value", gv, bv), ("loc", gl, bl), ("attn", ga, ba)):
+            assert torch.isfinite(got.float()).all(), f"grad_{name} not finite"
+            assert max_rel(got.float(), want) <= FWD_TOL_HALF, f"grad_{name} {max_rel(got.float(), want)}"
+        assert torch.all(ga[outside] == 0) and torch.all(gl[outside] == 0)
+
     # ------------------------------------------------------------- added cases
     def test_mixed_dtype_fp32_coords(self) -> None:
         """bf16 value with fp32 locations and weights (autocast-style inputs)."""
