@@ -276,12 +276,13 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
   const uint32_t NT = d->dim == 2 ? msda::kTileThreads<2> : msda::kTileThreads<3>;
   // 16-bit values: the tile kernel forms the sample gradients from staged region rows
   const bool tile_dots = s == 2;
-  // staged rows (grad_out and value, both in the value dtype): with tile_dots C * s rounded
-  // up to an odd number of 16-byte slots, so one chunk of random rows spreads over every
-  // bank slot
-  const uint32_t grow = tile_dots ? ((uint32_t)(d->channels * s) + 15u) / 32u * 32u + 16u
-                                  : (uint32_t)(d->channels * s);
-  const uint32_t vrow = tile_dots ? grow : 0u;
+  // staged rows, both in the value dtype: grad_out rows C * s bytes apart; value rows C * s
+  // rounded up to an odd number of 16-byte slots, so one chunk of random rows spreads over
+  // every bank slot (C2 tile kernel 237 -> 224 us). Padding the grad_out rows too spreads
+  // the dot products' reads of consecutive records' rows, but the LDS it takes lowers S
+  // (2D 256 -> 224, 3D 448 -> 416) and that costs more (224 -> 229 us, C5 653 -> 669 us).
+  const uint32_t grow = (uint32_t)(d->channels * s);
+  const uint32_t vrow = tile_dots ? ((uint32_t)(d->channels * s) + 15u) / 32u * 32u + 16u : 0u;
   const int ov = msda::tile_owner_vec(lay.vec_bytes / s, s);
   const int onv = d->channels / ov;
   int T[3];

@@ -1068,9 +1068,7 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
   const TileCoord tc = decode_tile(pl, geo, t, &lv);
 
   const uint32_t S = pl.S;
-  // bytes between staged grad_out rows (value dtype, C * s rounded up to an odd number of
-  // 16-byte slots, so the same chunk of consecutive records' rows falls in different banks)
-  const uint32_t grow = pl.grow;
+  const uint32_t grow = pl.grow;  // bytes between staged grad_out rows (value dtype)
   // bytes between staged value rows: an odd number of 16-byte slots, so the same chunk of
   // random rows falls in every slot of a bank row, not in every second or fourth one
   const uint32_t vrow = pl.vrow;

@@ -245,9 +245,8 @@ struct BwdPlan {
                                // else (fp32) the sample-gradient kernel gathers the corner rows
                                // per unit and bins the samples (fp32 rows leave too little LDS
                                // for the region: C2 fp32 backward 430 against 537 us)
-  uint32_t grow;               // bytes between the tile kernel's staged grad_out rows (value
-                               // dtype; with tile_dots C * s rounded up to an odd number of
-                               // 16-byte slots)
+  uint32_t grow;               // bytes between the tile kernel's staged grad_out rows (C * s,
+                               // value dtype)
   uint32_t vrow;               // bytes between the tile kernel's staged value rows (C * s
                                // rounded up to an odd number of 16-byte slots)
   uint32_t lds_g_bytes;        // bytes of the staged grad_out rows of a sub-batch
