@@ -365,6 +365,21 @@ def load_traffic(key: str):
     return e, None
 
 
+def load_ceiling(key: str):
+    """The forward's counter-backed ceiling from profiles/fwd_ceiling.json: its L2 request
+    counts (rocprofv3 TCC counters) served at the gather probes' L2 and MALL row rates, as
+    {"ms", "frac"} of the HBM roofline, or None."""
+    try:
+        e = json.loads((REPO / "profiles" / "fwd_ceiling.json").read_text()).get(key)
+    except (OSError, ValueError):
+        return None
+    if not isinstance(e, dict):
+        return None
+    return {"bound": "L2 line requests: hits at the L2 gather rate, misses at the MALL rate",
+            "l2_requests": e["l2_requests"], "l2_misses": e["l2_misses"],
+            "ms": e["ceiling_ms"], "frac": e["ceiling_frac"], "source": "profiles/fwd_ceiling.md"}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -450,6 +465,8 @@ def main():
                 "algorithmic_bytes_per_launch": kbytes, "avg_launch_ms": round(kms, 5)}
 
     roofline = roof(FWD_KERNEL, r["bytes"]["fwd"], r["fwd_ms"], "msda_fwd:c2_bf16")
+    # what bounds this design below the HBM roofline: its L2 line requests
+    roofline["ceiling"] = load_ceiling("msda_fwd:c2_bf16")
     roofline_bwd = roof(BWD_KERNELS, r["bytes"]["bwd"], r["bwd_ms"], "msda_bwd:c2_bf16")
 
     cpu = None
@@ -486,7 +503,7 @@ def main():
                    "B": 2, "H": 8, "C": 32, "levels": main_cfg["shapes"], "K": num_keys(main_cfg),
                    "Q": main_cfg["Q"], "P": 4, "clamp_grid": True, "clamp_eps": 1e-4},
         "c2_bf16": dict(summary(r), fwd_bwd_ms_gpu_shapes=round(c2_gpu_shapes_ms, 5)),
-        "also": {"c5_bf16_3d_4level": summary(r5),
+        "also": {"c5_bf16_3d_4level": dict(summary(r5), fwd_ceiling=load_ceiling("msda_fwd:c5_bf16")),
                  **{k: summary(v) for k, v in extra.items()},
                  "c3_bf16_decoder": {"fwd_ms": round(c3_fwd_ms, 5),
                                      "note": "msda2d_fwd through the Python API (host time included)"},
