@@ -345,6 +345,27 @@ class ParitySuite:
         _, gv, gl, ga = self.run_fwd_bwd(value, shapes, loc, attn, grad_out)
         self.check_grads(value, shapes, loc, attn, grad_out, gv, gl, ga)
 
+    @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+    @pytest.mark.parametrize("heads,ch", [(3, 3), (2, 48), (5, 16), (2, 128)])
+    def test_odd_heads_channels_half(self, heads, ch, dtype) -> None:
+        """16-bit values (the binned backward's tile kernel forms grad_loc / grad_attn from its
+        staged region rows) with channel counts that change the staged row sizes and owner
+        chunks (C=3: 6-byte rows; C=48: 96-byte rows, 6 of 8 lanes; C=128: tiles shrunk to fit
+        the owner items), odd head counts and 3 points per level (the generic count and fill
+        loops): every gradient against the float64 oracle on the upcast inputs."""
+        value, shapes, loc, attn = self.inputs(batch_size=2, num_queries=33, num_heads=heads,
+                                               dim_per_head=ch, num_levels=3, num_points=3)
+        value, loc, attn = (t.to(dtype) for t in (value, loc, attn))
+        vf, lf, af = (t.float() for t in (value, loc, attn))
+        out = self.fwd(*self.gpu(value), shapes, *self.gpu(loc, attn)).cpu()
+        assert max_rel(out.float(), brute.fwd(vf, shapes, lf, af, coord_f32=True)) <= FWD_TOL_HALF
+        g = torch.Generator().manual_seed(5)
+        grad_out = torch.randn(out.shape, generator=g).to(dtype)
+        _, gv, gl, ga = self.run_fwd_bwd(value, shapes, loc, attn, grad_out)
+        bv, _, ba = brute.bwd(vf, shapes, lf, af, grad_out.float(), coord_f32=True)
+        assert max_rel(gv.float(), bv) <= FWD_TOL_HALF and max_rel(ga.float(), ba) <= FWD_TOL_HALF
+        self.check_half_grad_loc(value, shapes, loc, attn, grad_out, gl)
+
     def test_wide_level_32bit_addressing(self) -> None:
         """A level whose row stride along y (2D) or z (3D) exceeds 2^23 bytes: corner offsets
         take the 32-bit multiply path instead of the 24-bit one, forward and backward."""
