@@ -464,8 +464,8 @@ void carve(char* ws, const msda::BwdSizes& z, msda::BwdBuffers* bf) {
   p += al(z.bin_start * 4);
   bf->chunk_off = reinterpret_cast<uint32_t*>(p);
   p += al(z.chunk_off * 4);
-  bf->chunk_tile = reinterpret_cast<uint32_t*>(p);
-  p += al(z.chunk_tile * 4);
+  bf->chunks = reinterpret_cast<uint4*>(p);
+  p += al(z.chunk_words * 4);
   bf->records = reinterpret_cast<uint32_t*>(p);
   p += al(z.record_words * 4);
   bf->scratch = reinterpret_cast<float*>(p);

@@ -675,7 +675,9 @@ __global__ __launch_bounds__(kBlock) void bwd_colscan_kernel(const BwdPlan pl, c
 // ------------------------------------------------------------------ 3: plan
 // One workgroup per (batch, head-group): the record totals of the group's tiles become
 // first-record offsets, each tile is cut into max(1, ceil(n / R)) chunks (an empty tile
-// still gets one chunk, which writes its zeros), and the chunk -> tile table is filled.
+// still gets one chunk, which writes its zeros), and each chunk gets its descriptor
+// {tile, first record, end record, chunks of the tile}, so a tile workgroup starts from one
+// load instead of three dependent ones.
 // Each workgroup first sums the totals of the tiles of all earlier groups (coalesced loads
 // and a workgroup reduction), then scans its own tiles, each thread a contiguous range.
 // (One workgroup for all tiles spent 14 us of C5's backward on the stores of one CU.)
@@ -726,7 +728,8 @@ __global__ __launch_bounds__(kPlanThreads) void bwd_plan_kernel(const BwdPlan pl
     const uint32_t nch = chunks(n);
     bf.bin_start[t] = pn;
     bf.chunk_off[t] = pc;
-    for (uint32_t k = 0; k < nch; ++k) bf.chunk_tile[pc + k] = t;
+    for (uint32_t k = 0; k < nch; ++k)
+      bf.chunks[pc + k] = make_uint4(t, pn + k * pl.R, min(pn + n, pn + (k + 1) * pl.R), nch);
     pn += n;
     pc += nch;
   };
@@ -1059,11 +1062,8 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
     c = x * per + slot;
     if (c >= total) return;
   }
-  const uint32_t t = bf.chunk_tile[c];
-  const uint32_t off = bf.chunk_off[t];
-  const uint32_t nch = bf.chunk_off[t + 1] - off;
-  const uint32_t beg = bf.bin_start[t] + (c - off) * pl.R;
-  const uint32_t end = min(bf.bin_start[t + 1], beg + pl.R);
+  const uint4 cd = bf.chunks[c];
+  const uint32_t t = cd.x, beg = cd.y, end = cd.z, nch = cd.w;
   BwdLevel lv;
   const TileCoord tc = decode_tile(pl, geo, t, &lv);
 
@@ -1093,17 +1093,35 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
   // the region's value rows -> LDS, once per chunk: every corner of the chunk's samples
   // (their <grad_out, v_c> dot products give grad_attn and grad_loc)
   if constexpr (DOTS) {
+    // in rounds of KS items per thread, every load of a round issued before its LDS stores
+    // (one storing each load before the next was issued left the chunk's prologue waiting
+    // for KS memory round trips in a row)
+    constexpr int KS = 4;
     const TV* val = static_cast<const TV*>(bf.value);
     const int exy = rg.ex * rg.ey;
-    for (int i = tid; i < ncell_r * (int)nvec; i += NT) {
-      const int cell = (int)fdiv((uint32_t)i, pl.div_nvec), ch = i - cell * (int)nvec;
-      const int rz = cell / exy, rxy = cell - rz * exy;
-      const int ry = rxy / rg.ex, rx = rxy - ry * rg.ex;
-      const uint32_t row = (uint32_t)lv.start + ((uint32_t)(tc.Z0 + rz) * lv.H + (tc.Y0 + ry)) * lv.W +
-                           (tc.X0 + rx);
-      const size_t e = pl.head_major ? (((size_t)tc.b * pl.H + tc.h) * pl.K + row) * pl.C
-                                     : (((size_t)tc.b * pl.K + row) * pl.H + tc.h) * pl.C;
-      *reinterpret_cast<RawVec<VB>*>(s_v + cell * vrow + ch * VB) = glb_load<VB>(val + e + ch * VEC);
+    const int nit = ncell_r * (int)nvec;
+    for (int i0 = tid; i0 < nit; i0 += KS * NT) {
+      RawVec<VB> v[KS];
+      uint32_t dst[KS];
+#pragma unroll
+      for (int k = 0; k < KS; ++k) {
+        const int i = i0 + k * NT;
+        dst[k] = 0xffffffffu;
+        if (i < nit) {
+          const int cell = (int)fdiv((uint32_t)i, pl.div_nvec), ch = i - cell * (int)nvec;
+          const int rz = cell / exy, rxy = cell - rz * exy;
+          const int ry = rxy / rg.ex, rx = rxy - ry * rg.ex;
+          const uint32_t row = (uint32_t)lv.start +
+                               ((uint32_t)(tc.Z0 + rz) * lv.H + (tc.Y0 + ry)) * lv.W + (tc.X0 + rx);
+          const size_t e = pl.head_major ? (((size_t)tc.b * pl.H + tc.h) * pl.K + row) * pl.C
+                                         : (((size_t)tc.b * pl.K + row) * pl.H + tc.h) * pl.C;
+          v[k] = glb_load<VB>(val + e + ch * VEC);
+          dst[k] = (uint32_t)cell * vrow + (uint32_t)ch * VB;
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < KS; ++k)
+        if (dst[k] != 0xffffffffu) *reinterpret_cast<RawVec<VB>*>(s_v + dst[k]) = v[k];
     }
   }
 
@@ -1632,7 +1650,7 @@ BwdSizes bwd_sizes(const BwdPlan& pl, uint64_t samples, int dim) {
   z.tile_n = (uint64_t)pl.T_cap + 1;
   z.bin_start = (uint64_t)pl.T_cap + 1;
   z.chunk_off = (uint64_t)pl.T_cap + 1;
-  z.chunk_tile = pl.max_chunks;
+  z.chunk_words = (uint64_t)pl.max_chunks * 4u;
   z.record_words = binned ? (samples > 0 ? samples : 1) * (uint64_t)(dim + 2) : 0u;
   z.scratch_floats = binned ? (uint64_t)pl.max_chunks * pl.rcells * pl.C : 0u;
   // atomic path: one fp32 sum per grad_value element of a launch (groups << hg_log2 =
@@ -1641,7 +1659,7 @@ BwdSizes bwd_sizes(const BwdPlan& pl, uint64_t samples, int dim) {
   z.geom_bytes = sizeof(BwdGeom);
   auto al = [](uint64_t b) { return (b + 255) & ~(uint64_t)255; };
   z.total_bytes = al(z.counts * 4) + al(z.tile_n * 4) + al(z.bin_start * 4) + al(z.chunk_off * 4) +
-                  al(z.chunk_tile * 4) + al(z.record_words * 4) + al(z.scratch_floats * 4) +
+                  al(z.chunk_words * 4) + al(z.record_words * 4) + al(z.scratch_floats * 4) +
                   al(z.sum_floats * 4) + al(z.geom_bytes);
   return z;
 }

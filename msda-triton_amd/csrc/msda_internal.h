@@ -269,7 +269,7 @@ struct BwdBuffers {
   uint32_t* tile_n;      // T: record total of each tile (column scan -> plan)
   uint32_t* bin_start;   // T + 1: first record of each tile
   uint32_t* chunk_off;   // T + 1: first chunk of each tile; [T] = number of chunks
-  uint32_t* chunk_tile;  // max_chunks: tile of each chunk
+  uint4* chunks;         // max_chunks: {tile, first record, end record, chunks of the tile}
   uint32_t* records;     // (DIM + 2) words per record: id | flags, u_x, u_y[, u_z], attn
   float* scratch;        // max_chunks * rcells * C fp32 partials
   float* sums;           // atomic path: fp32 sums in the gathered value's layout
@@ -277,7 +277,7 @@ struct BwdBuffers {
 };
 
 struct BwdSizes {
-  uint64_t counts, tile_n, bin_start, chunk_off, chunk_tile, record_words, scratch_floats, sum_floats;
+  uint64_t counts, tile_n, bin_start, chunk_off, chunk_words, record_words, scratch_floats, sum_floats;
   uint64_t geom_bytes;
   uint64_t total_bytes;
 };
