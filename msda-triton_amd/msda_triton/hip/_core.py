@@ -39,11 +39,9 @@ _CPU_ID_CACHE: OrderedDict = OrderedDict()
 
 
 def _raw_bytes(t: torch.Tensor):
-    """The raw bytes of a small CPU tensor (None if it has no plain numpy view)."""
-    try:
-        return t.detach().numpy().tobytes()
-    except (RuntimeError, TypeError):
-        return None
+    """The raw bytes of a small contiguous CPU tensor, read straight from its memory (None
+    for other layouts)."""
+    return ctypes.string_at(t.data_ptr(), t.nbytes) if t.is_contiguous() else None
 
 
 def validate_inputs(name: str, dim: int, value: torch.Tensor, value_spatial_shapes: torch.Tensor,
@@ -256,6 +254,26 @@ def _stream(device: torch.device) -> int:
     return torch._C._cuda_getCurrentRawStream(device.index)
 
 
+# Forward descriptors and their workspace sizes, keyed by the problem (shapes, dtypes, clamp):
+# a loop over one problem builds the ctypes descriptor and asks for its workspace once.
+_FWD_DESC_CACHE: OrderedDict = OrderedDict()
+
+
+def _fwd_desc(dim: int, value: torch.Tensor, loc: torch.Tensor, cdt: torch.dtype, clamp_grid: bool,
+              clamp_eps: float):
+    """(msda_desc, forward workspace bytes) for the problem, cached."""
+    key = (dim, value.shape, loc.shape, value.dtype, cdt, bool(clamp_grid), float(clamp_eps))
+    hit = _FWD_DESC_CACHE.get(key)
+    if hit is not None:
+        return hit
+    desc = make_desc(dim, value, loc, cdt, clamp_grid, clamp_eps)
+    ws_bytes = int(_lib.load().msda_fwd_workspace_bytes(ctypes.byref(desc)))
+    _FWD_DESC_CACHE[key] = (desc, ws_bytes)
+    if len(_FWD_DESC_CACHE) > _LEVEL_CACHE_MAX:
+        _FWD_DESC_CACHE.popitem(last=False)
+    return desc, ws_bytes
+
+
 def forward(dim: int, value: torch.Tensor, levels: Levels, loc: torch.Tensor, attn: torch.Tensor,
             clamp_grid: bool, clamp_eps: float):
     """Launch msda_fwd. Returns (out, value_c, loc_c, attn_c, value_hm): the output, the
@@ -270,9 +288,8 @@ def forward(dim: int, value: torch.Tensor, levels: Levels, loc: torch.Tensor, at
     bsz, _, num_heads, ch = value.shape
     num_queries = loc.shape[1]
     out = torch.empty((bsz, num_queries, num_heads * ch), device=value.device, dtype=value.dtype)
-    desc = make_desc(dim, value_c, loc_c, cdt, clamp_grid, clamp_eps)
     # optional workspace: a head-major copy of value for large, line-sharing value slices
-    ws_bytes = int(lib.msda_fwd_workspace_bytes(ctypes.byref(desc)))
+    desc, ws_bytes = _fwd_desc(dim, value_c, loc_c, cdt, clamp_grid, clamp_eps)
     ws = torch.empty(ws_bytes, device=value.device, dtype=torch.uint8) if ws_bytes else None
     with _on_device(value.device):
         rc = lib.msda_fwd(ctypes.byref(desc), value_c.data_ptr(), levels.spatial.data_ptr(),
