@@ -1155,20 +1155,19 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
     for (uint32_t m0 = 0; m0 < nvec; m0 += GB) {
       RawVec<VB> gr[GB];
       uint32_t dst[GB];
+      // every load unconditional, so all of them are in flight together (loads under a
+      // per-lane branch were each issued only after the previous one had returned): chunks past
+      // the row's end re-load its last chunk, rows past the sub-batch's end load the row of
+      // query 0 (q is 0 without a record), and neither is stored
 #pragma unroll
       for (int k = 0; k < GB; ++k) {
-        const uint32_t m = m0 + (uint32_t)k;
-        dst[k] = 0xffffffffu;
-        if (m < nvec) {  // uniform
-          const uint32_t jj = m * kWave + (uint32_t)lane;
-          const uint32_t lr = fdiv(jj, pl.div_nvec), ch = jj - lr * nvec;
-          const uint32_t qq = (uint32_t)__builtin_amdgcn_ds_bpermute((int)(lr << 2), (int)q);
-          const uint32_t r = (uint32_t)wv * kWave + lr;
-          if (r < nrec) {
-            gr[k] = glb_load<VB>(gout + (size_t)qq * grad_q_stride + ch * VEC);
-            dst[k] = r * grow + ch * (uint32_t)VB;
-          }
-        }
+        const uint32_t m = min(m0 + (uint32_t)k, nvec - 1u);
+        const uint32_t jj = m * kWave + (uint32_t)lane;
+        const uint32_t lr = fdiv(jj, pl.div_nvec), ch = jj - lr * nvec;
+        const uint32_t qq = (uint32_t)__builtin_amdgcn_ds_bpermute((int)(lr << 2), (int)q);
+        const uint32_t r = (uint32_t)wv * kWave + lr;
+        gr[k] = glb_load<VB>(gout + (size_t)qq * grad_q_stride + ch * VEC);
+        dst[k] = m0 + (uint32_t)k < nvec && r < nrec ? r * grow + ch * (uint32_t)VB : 0xffffffffu;
       }
       if (m0 == 0 && has) {
         // the owner's corners, while the first row loads are in flight
