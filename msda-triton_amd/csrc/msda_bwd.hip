@@ -160,6 +160,31 @@ __device__ inline int region_cell(const Region& rg, int ox, int oy, int oz) {
   return (oz * rg.ey + oy) * rg.ex + ox;
 }
 
+// Region cell -> (x, y, z) offsets within the compact region. The quotients are formed as
+// trunc((n + 0.5) * (1 / d)): for n < 2^20 the product's rounding error is below
+// 2^-3 / d, while (n + 0.5) / d lies at least 0.5 / d from an integer, so the result is
+// exact, in three instructions instead of a twenty-instruction integer division.
+struct RegionSplit {
+  float rxy, rx;  // 1 / (ex * ey), 1 / ex
+  int exy, ex;
+};
+
+__device__ inline RegionSplit region_split(const Region& rg) {
+  RegionSplit r;
+  r.exy = rg.ex * rg.ey;
+  r.ex = rg.ex;
+  r.rxy = 1.0f / (float)r.exy;
+  r.rx = 1.0f / (float)r.ex;
+  return r;
+}
+
+__device__ inline void split_cell(const RegionSplit& r, int cell, int& rx, int& ry, int& rz) {
+  rz = (int)(((float)cell + 0.5f) * r.rxy);
+  const int rxy = cell - rz * r.exy;
+  ry = (int)(((float)rxy + 0.5f) * r.rx);
+  rx = rxy - ry * r.ex;
+}
+
 // Unit of a bin workgroup: the wi-th of the upw units of workgroup w of group g.
 struct BinUnit {
   uint32_t q, hsub, b, h;
@@ -1098,7 +1123,7 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
     // for KS memory round trips in a row)
     constexpr int KS = 4;
     const TV* val = static_cast<const TV*>(bf.value);
-    const int exy = rg.ex * rg.ey;
+    const RegionSplit rs = region_split(rg);
     const int nit = ncell_r * (int)nvec;
     for (int i0 = tid; i0 < nit; i0 += KS * NT) {
       RawVec<VB> v[KS];
@@ -1109,8 +1134,8 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
         dst[k] = 0xffffffffu;
         if (i < nit) {
           const int cell = (int)fdiv((uint32_t)i, pl.div_nvec), ch = i - cell * (int)nvec;
-          const int rz = cell / exy, rxy = cell - rz * exy;
-          const int ry = rxy / rg.ex, rx = rxy - ry * rg.ex;
+          int rx, ry, rz;
+          split_cell(rs, cell, rx, ry, rz);
           const uint32_t row = (uint32_t)lv.start +
                                ((uint32_t)(tc.Z0 + rz) * lv.H + (tc.Y0 + ry)) * lv.W + (tc.X0 + rx);
           const size_t e = pl.head_major ? (((size_t)tc.b * pl.H + tc.h) * pl.K + row) * pl.C
@@ -1347,6 +1372,7 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
     lds_sync();  // LDS of this sub-batch is reused by the next one
   }
 
+  const RegionSplit rs_out = region_split(rg);
   // write the region: interior cells of a one-chunk tile directly in the value dtype;
   // edge cells, halo cells inside the level and all cells of a split tile as fp32 partials
   // for the fold kernel
@@ -1355,9 +1381,8 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
     const int it = (int)threadIdx.x + m * NT;
     if (it >= ncell_r * onv) continue;
     const int cell = (int)fdiv((uint32_t)it, pl.div_onv), ch = it - cell * onv;
-    const int exy = rg.ex * rg.ey;  // compact region extents: once per chunk, plain division
-    const int rz = cell / exy, rxy = cell - rz * exy;
-    const int ry = rxy / rg.ex, rx = rxy - ry * rg.ex;
+    int rx, ry, rz;
+    split_cell(rs_out, cell, rx, ry, rz);
     const int x = tc.X0 + rx, y = tc.Y0 + ry, z = tc.Z0 + rz;
     const bool owned = rx < pl.TX && ry < pl.TY && rz < pl.TZ;
     const bool interior = owned && rx > 0 && ry > 0 && (DIM == 2 || rz > 0);
