@@ -270,7 +270,7 @@ struct BwdBuffers {
   uint32_t* bin_start;   // T + 1: first record of each tile
   uint32_t* chunk_off;   // T + 1: first chunk of each tile; [T] = number of chunks
   uint4* chunks;         // max_chunks: {tile, first record, end record, chunks of the tile}
-  uint32_t* records;     // (DIM + 2) words per record: id | flags, u_x, u_y[, u_z], attn
+  uint32_t* records;     // at most DIM + 2 words per record (rec_words in msda_bwd.hip)
   float* scratch;        // max_chunks * rcells * C fp32 partials
   float* sums;           // atomic path: fp32 sums in the gathered value's layout
   const BwdGeom* geom;   // level geometry of the launch (written by the first kernel)
