@@ -1223,7 +1223,7 @@ __global__ __launch_bounds__(kTileThreads<DIM>, kTileWavesPerSimd) void bwd_tile
     uint32_t* s_cnt = s_cnt2 + par * ncp;
     const bool has = (uint32_t)tid < nrec;
 
-    // 1. grad_out rows -> LDS as fp32; corner ranks
+    // 1. grad_out rows -> LDS in the value dtype; corner ranks
     const uint32_t q = has ? fdiv(rec[0] & kRecIdMask, pl.div_p) : 0u;
     Sample<DIM> sm;
     uint32_t slot[NC];  // (region cell << 16) | rank within the cell, or ~0u: no entry
