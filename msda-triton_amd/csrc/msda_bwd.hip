@@ -832,14 +832,22 @@ __global__ __launch_bounds__(kBlock) void bwd_fill_kernel(const BwdPlan pl, cons
   auto finish_round = [&](const uint32_t (&key)[KP], const uint32_t (&rw)[KP][RW], uint32_t b0,
                           uint32_t b1) {
     lds_sync();
-    uint32_t carry = 0;
-    for (uint32_t c0 = b0; c0 < b1; c0 += kBlock) {
-      const uint32_t i = c0 + threadIdx.x;
-      const uint32_t v = i < b1 ? s_cnt[i] : 0u;
-      uint32_t tot;
-      const uint32_t ex = block_excl_scan<kBlock>(v, s_w, &tot);
-      if (i < b1) s_cnt[i] = carry + ex;
-      carry += tot;
+    // exclusive scan of the round's bin counts: each thread sums a run of consecutive bins,
+    // one block scan of those sums, then each thread writes its run's offsets (one block
+    // scan, two barriers, however many bins; a block scan per 256 bins took ten barriers
+    // per round at C5's 1170 bins)
+    uint32_t carry;
+    {
+      const uint32_t per = (b1 - b0 + kBlock - 1) / kBlock;
+      const uint32_t j0 = min(b1, b0 + threadIdx.x * per), j1 = min(b1, j0 + per);
+      uint32_t sum = 0;
+      for (uint32_t j = j0; j < j1; ++j) sum += s_cnt[j];
+      uint32_t run = block_excl_scan<kBlock>(sum, s_w, &carry);
+      for (uint32_t j = j0; j < j1; ++j) {
+        const uint32_t v = s_cnt[j];
+        s_cnt[j] = run;
+        run += v;
+      }
     }
     lds_sync();
 #pragma unroll
