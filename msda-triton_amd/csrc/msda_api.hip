@@ -430,7 +430,7 @@ int plan_bwd(const msda_desc* d, const int32_t* hs, const void* const* ptrs, int
   pl.grid_chunks = (pl.max_chunks + pl.xcds - 1) / pl.xcds * pl.xcds;
   pl.value_bytes = (uint32_t)(nb * (uint64_t)d->num_keys * d->num_heads * d->channels * s);
   pl.grad_loc_elems = samples * (uint64_t)d->dim;
-  out->sz = msda::bwd_sizes(pl, samples, d->dim);
+  out->sz = msda::bwd_sizes(pl, samples, d->dim, elem_bytes(d->coord_dtype));
   msda::GeomArgs& ga = out->ga;
   ga.dim = d->dim;
   ga.L = d->num_levels;

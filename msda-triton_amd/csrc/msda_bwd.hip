@@ -781,7 +781,7 @@ __global__ __launch_bounds__(kPlanThreads) void bwd_plan_kernel(const BwdPlan pl
 // in place of 16 / 20: the fill writes and the tile kernel reads 25% / 40% fewer bytes.)
 template <int DIM, typename EC>
 constexpr int rec_words() {
-  return EC::kBytes == 2 ? 3 : DIM + 2;
+  return record_words(DIM, EC::kBytes);
 }
 
 template <typename E>
@@ -1724,7 +1724,7 @@ bool bwd_supported(int dim, int vdt, int cdt, int vec_bytes) {
   return get_bwd(dim, vdt, cdt, vec_bytes) != nullptr;
 }
 
-BwdSizes bwd_sizes(const BwdPlan& pl, uint64_t samples, int dim) {
+BwdSizes bwd_sizes(const BwdPlan& pl, uint64_t samples, int dim, int coord_bytes) {
   BwdSizes z;
   const bool binned = !pl.static_atomic;
   const bool sums = pl.static_atomic || pl.fallback;
@@ -1733,7 +1733,7 @@ BwdSizes bwd_sizes(const BwdPlan& pl, uint64_t samples, int dim) {
   z.bin_start = (uint64_t)pl.T_cap + 1;
   z.chunk_off = (uint64_t)pl.T_cap + 1;
   z.chunk_words = (uint64_t)pl.max_chunks * 4u;
-  z.record_words = binned ? (samples > 0 ? samples : 1) * (uint64_t)(dim + 2) : 0u;
+  z.record_words = binned ? (samples > 0 ? samples : 1) * (uint64_t)record_words(dim, coord_bytes) : 0u;
   z.scratch_floats = binned ? (uint64_t)pl.max_chunks * pl.rcells * pl.C : 0u;
   // atomic path: one fp32 sum per grad_value element of a launch (groups << hg_log2 =
   // batches * H)

@@ -20,6 +20,10 @@ constexpr int kTileThreads = DIM == 2 ? 256 : 512;
 constexpr int tile_owner_vec(int vec, int eb) { return vec < 16 / eb ? vec : 16 / eb; }
 // (region cell, channel chunk) owner items per tile thread: 20-24 fp32 accumulators
 constexpr int tile_max_items(int ov) { return ov >= 8 ? 3 : 5; }
+// words per backward record: 16-bit coordinates 3 (id | flags, then the raw 16-bit
+// location and weight two to a word), fp32 coordinates dim + 2 (id | flags, the pixel
+// coordinates and the weight)
+constexpr int record_words(int dim, int coord_bytes) { return coord_bytes == 2 ? 3 : dim + 2; }
 constexpr int kTileWavesPerSimd = 4;  // tile-kernel occupancy target (128 VGPRs)
 constexpr int kFillStage = 2048;      // records staged in LDS per fill round
 constexpr int kGradThreads = 256;     // threads of the backward count, fill and atomic kernels
@@ -270,7 +274,7 @@ struct BwdBuffers {
   uint32_t* bin_start;   // T + 1: first record of each tile
   uint32_t* chunk_off;   // T + 1: first chunk of each tile; [T] = number of chunks
   uint4* chunks;         // max_chunks: {tile, first record, end record, chunks of the tile}
-  uint32_t* records;     // at most DIM + 2 words per record (rec_words in msda_bwd.hip)
+  uint32_t* records;     // record_words(DIM, coordinate bytes) words per record
   float* scratch;        // max_chunks * rcells * C fp32 partials
   float* sums;           // atomic path: fp32 sums in the gathered value's layout
   const BwdGeom* geom;   // level geometry of the launch (written by the first kernel)
@@ -283,7 +287,7 @@ struct BwdSizes {
 };
 
 // Workspace element counts for a plan, `samples` samples and dimension dim.
-BwdSizes bwd_sizes(const BwdPlan& pl, uint64_t samples, int dim);
+BwdSizes bwd_sizes(const BwdPlan& pl, uint64_t samples, int dim, int coord_bytes);
 
 // Clear `bytes` bytes of device memory with a fill kernel (no hipMemset node in graphs).
 hipError_t launch_zero_bytes(void* p, size_t bytes, hipStream_t s);

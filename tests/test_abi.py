@@ -148,7 +148,7 @@ def test_bwd_levels_beyond_binning_plan_atomic_path():
     ws = lib.msda_bwd_workspace_bytes(ctypes.byref(many), _shapes((32, 32)))
     assert 32 * 32 * 32 * 4 <= ws < q * 16 * 4, _lib.last_error()
     fewer = _desc(batch=1, num_keys=32 * 32, num_queries=q - 2, num_levels=1, num_points=16,
-                  num_heads=1)  # 2^27 - 16 samples: binned, 16-byte records
+                  num_heads=1)  # 2^27 - 16 samples: binned, 12-byte records (bf16)
     assert lib.msda_bwd_workspace_bytes(ctypes.byref(fewer), _shapes((32, 32))) > q * 16 * 4
 
 
