@@ -237,6 +237,31 @@ class ParitySuite:
         assert max_rel(gv.float(), bv) <= FWD_TOL_HALF and max_rel(ga.float(), ba) <= FWD_TOL_HALF
 
     @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+    def test_half_precision_lattice_points(self, dtype) -> None:
+        """16-bit locations on an exact lattice of k / (2 * largest extent) over power-of-two
+        levels, so every sample's pixel coordinate is an exact integer, half or quarter
+        (corner weights 0 / 1 and ties of floor): the tile kernel re-derives each sample's
+        corners from its record's raw 16-bit location, and must pick the fill's corners for
+        every one of them. All gradients against the float64 oracle with the kernels' fp32
+        coordinate rounding."""
+        ss = [(32, 32), (16, 16), (8, 8)] if self.dim == 2 else [(8, 16, 16), (4, 8, 8)]
+        value, shapes, loc, attn = self.inputs(batch_size=2, num_queries=60, num_heads=4,
+                                               dim_per_head=32, spatial_shapes=ss)
+        n = 2 * max(max(s) for s in ss)
+        g = torch.Generator().manual_seed(11)
+        loc = torch.randint(0, n + 1, loc.shape, generator=g).float() / n
+        value, loc, attn = (t.to(dtype) for t in (value, loc, attn))
+        assert torch.equal(loc.float() * n, (loc.float() * n).round())  # exact in 16 bits
+        grad_out = torch.randn(2, 60, 4 * 32, generator=g).to(dtype)
+        out, gv, gl, ga = self.run_fwd_bwd(value, shapes, loc, attn, grad_out)
+        ref = brute.fwd(value.float(), shapes, loc.float(), attn.float(), coord_f32=True)
+        assert max_rel(out.float(), ref) <= FWD_TOL_HALF
+        self.check_half_grad_loc(value, shapes, loc, attn, grad_out, gl)
+        bv, _, ba = brute.bwd(value.float(), shapes, loc.float(), attn.float(), grad_out.float(),
+                              coord_f32=True)
+        assert max_rel(gv.float(), bv) <= FWD_TOL_HALF and max_rel(ga.float(), ba) <= FWD_TOL_HALF
+
+    @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
     def test_half_precision_no_clamp_outside_levels(self, dtype) -> None:
         """16-bit inputs without the grid clamp, locations over [-0.3, 1.3]: samples with no
         corner inside their level get exactly zero grad_loc and grad_attn (in the binned
